@@ -1,0 +1,111 @@
+"""ctypes binding of the loom-hip C ABI (``include/loom_hip.h``).
+
+The library is loaded from the in-tree build ``attnarc_amd/_build/
+libloom_hip.so``. There is no fallback: if the library is missing or fails to
+load, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from . import build as _build
+
+LIB_PATH = _build.LIB_PATH
+
+SUCCESS = 0
+INVALID_ARGUMENT = 1
+UNSUPPORTED = 2
+LAUNCH_ERROR = 3
+UNAVAILABLE = 4
+
+KV_CACHE_NATIVE = 0
+KV_CACHE_FP8_E4M3 = 1
+
+F32, F16, BF16 = 0, 1, 2
+PAGED_DECODE_ATTENTION = 9
+KERNEL_DECODE, KERNEL_MERGE = 0, 1
+
+P = ctypes.c_void_p
+U32 = ctypes.c_uint32
+U64 = ctypes.c_uint64
+F = ctypes.c_float
+
+# (name, argtypes, restype) for every symbol declared in include/loom_hip.h.
+_BASE = [P, P, P, P, P, P] + [U32] * 7 + [U64, U64, U32, U32, F, P]
+_SPLIT = [P, P, P, P, P, P, P, U64] + [U32] * 7 + [U64, U64, U32, U32, F, P]
+_EXT = [P, P, P, P, P, P, P, P, P, P, U64] + [U32] * 9 + [U64] * 6 + [U32, U32, U32, F, P]
+SIGNATURES = {
+    "loom_hip_status_string": ([ctypes.c_int], ctypes.c_char_p),
+    "loom_hip_paged_decode_attention_f32": (_BASE, ctypes.c_int),
+    "loom_hip_paged_decode_attention_f16": (_BASE, ctypes.c_int),
+    "loom_hip_paged_decode_attention_bf16": (_BASE, ctypes.c_int),
+    "loom_hip_paged_decode_attention_split_k_workspace_elements": ([U32] * 6, U64),
+    "loom_hip_paged_decode_attention_split_k_f32": (_SPLIT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_split_k_f16": (_SPLIT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_split_k_bf16": (_SPLIT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_extended_workspace_elements": ([U32] * 5, U64),
+    "loom_hip_paged_decode_attention_extended_f32": (_EXT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_extended_f16": (_EXT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_extended_bf16": (_EXT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_supports": (
+        [U32] * 11 + [F, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p)],
+        ctypes.c_int,
+    ),
+    "loom_hip_backend_name": ([], ctypes.c_char_p),
+    "loom_hip_abi_version": ([], U32),
+    "loom_hip_last_error_message": ([], ctypes.c_char_p),
+    "loom_hip_launch_count": ([U32, ctypes.POINTER(U64)], ctypes.c_int),
+    "loom_hip_reset_launch_count": ([U32], ctypes.c_int),
+    "loom_hip_kernel_timing_enable": ([U32], ctypes.c_int),
+    "loom_hip_kernel_timing_read": ([U32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(U64)], ctypes.c_int),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class LoomHipError(RuntimeError):
+    """A non-success status from the loom-hip C ABI."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+def lib() -> ctypes.CDLL:
+    """Load the in-tree HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise ImportError(
+                    f"loom-hip native library not found at {LIB_PATH}; "
+                    "run `python -m attnarc_amd.build` (or __graft_entry__.build())"
+                )
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (argtypes, restype) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
+            _lib = handle
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().loom_hip_status_string(status).decode()
+
+
+def last_error() -> str:
+    return lib().loom_hip_last_error_message().decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != SUCCESS:
+        raise LoomHipError(
+            status, f"{what} failed: {status_string(status)}: {last_error()}"
+        )

@@ -1,0 +1,44 @@
+"""Build recipe of the in-tree HIP library ``_build/libloom_hip.so`` (gfx950).
+
+hipcc compiles the kernels and the C ABI in one translation unit. Packed FP32
+instruction selection is disabled (``-packed-fp32-ops``) for every HIP
+translation unit built here.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+SOURCE = os.path.join(PKG_DIR, "csrc", "paged_decode_attention.hip")
+LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+OFFLOAD_ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{os.path.join(REPO_DIR, 'include')}",
+]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the library; returns its path. Raises on compiler failure."""
+    os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [HIPCC, *HIPCC_FLAGS, SOURCE, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,1550 @@
+// Paged MQA/GQA decode attention for MI355X (gfx950).
+//
+// Semantics: crates/loom-kernels/src/attention.rs:270-357 (one query token
+// per sequence, softmax(scale * q.k) over the sequence's paged K, weighted sum
+// of paged V). The launch ABI is include/loom_hip.h, a one-for-one
+// replacement of the paged-decode part of
+// crates/loom-cuda-sys/cuda/include/loom_cuda.h:175-250 plus extensions.
+//
+// Kernels
+//   decode_mfma_kernel   D = Dv = 128, 16-bit query, native 16-bit or FP8
+//                        E4M3FN cache, power-of-two block size. One
+//                        workgroup per (partition, KV head, sequence); each
+//                        wave streams 32-token chunks: K is loaded straight
+//                        into the MFMA operand layout, V is staged through a
+//                        swizzled LDS tile and read back transposed, and both
+//                        QK^T and PV run on v_mfma_f32_16x16x32_{bf16,f16}
+//                        with the whole GQA group (up to 32 heads) held in
+//                        registers, so every K/V byte is read once.
+//   decode_vector_kernel any shape and dtype (including F32); fp32 VALU with
+//                        wave-wide reductions. Covers the general contract.
+//   merge_kernel         stable log-sum-exp merge of per-partition states
+//                        (the math of paged_decode_attention.cu:780-852).
+//
+// Both decode kernels keep an online softmax in base-2 units (scores are
+// multiplied by scale * log2(e)) and reduce the waves of a workgroup in LDS.
+// A workgroup whose partition is the whole sequence writes the output (and
+// optional LSE) directly; otherwise it writes (m, l, o[Dv]) to the caller's
+// F32 workspace and merge_kernel finishes.
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <mutex>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#include "../../include/loom_hip.h"
+
+namespace {
+
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Launch arguments shared by all kernels (passed by value as kernarg).
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+  const void* query;
+  const void* key_cache;
+  const void* value_cache;
+  const float* key_scales;
+  const float* value_scales;
+  const int32_t* block_tables;
+  const int32_t* sequence_lengths;
+  void* output;
+  float* lse;
+  float* ws_ml;  // [rows][parts][2] = (m in log2 units, l)
+  float* ws_o;   // [rows][parts][Dv], unnormalised, relative to m
+  uint64_t k_block, k_page, k_head;  // element strides of the key cache
+  uint64_t v_block, v_page, v_head;  // element strides of the value cache
+  uint32_t query_heads;
+  uint32_t kv_heads;
+  uint32_t group;  // query heads per KV head
+  uint32_t head_size;
+  uint32_t value_head_size;
+  uint32_t block_size;
+  uint32_t block_shift;  // log2(block_size) when it is a power of two
+  uint32_t max_blocks;
+  uint32_t partition_tokens;
+  uint32_t parts;  // partitions per (sequence, head); 1 = write output directly
+  uint32_t scale_stride;
+  uint32_t grid_y;  // decode kernels: work items per sequence besides partitions
+  float score_scale_log2;  // scale * log2(e)
+};
+
+// ---------------------------------------------------------------------------
+// Element types.
+// ---------------------------------------------------------------------------
+struct F32Elem {
+  using T = float;
+  static __device__ __forceinline__ float to_f(float x) { return x; }
+  static __device__ __forceinline__ float from_f(float x) { return x; }
+};
+
+struct F16Elem {
+  using T = uint16_t;
+  static __device__ __forceinline__ float to_f(uint16_t x) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+  static __device__ __forceinline__ uint16_t from_f(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  }
+};
+
+struct Bf16Elem {
+  using T = uint16_t;
+  static __device__ __forceinline__ float to_f(uint16_t x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+  static __device__ __forceinline__ uint16_t from_f(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));  // RNE
+  }
+};
+
+// OCP FP8 E4M3FN decode from its definition (quantization.rs:13-29):
+// subnormal m * 2^-9, normal (1 + m/8) * 2^(e-7), 0x7f/0xff NaN.
+struct Fp8Elem {
+  using T = uint8_t;
+  static __device__ __forceinline__ float to_f(uint8_t b) {
+    const uint32_t mag = b & 0x7fU;
+    const uint32_t e = mag >> 3;
+    const uint32_t m = mag & 7U;
+    float v = e == 0U ? static_cast<float>(m) * 0x1p-9f
+                      : __uint_as_float(((e + 120U) << 23) | (m << 20));
+    v = mag == 0x7fU ? __builtin_nanf("") : v;
+    return (b & 0x80U) ? -v : v;
+  }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_fence_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  return 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// General kernel: any head size, dtype, stride and group size.
+// grid.x = parts * grid_y * sequences, grid_y = kv_heads * head_chunks *
+// value_tiles; 256 threads (4 waves). Each wave walks every fourth token of
+// the partition; per token the lanes split the head dimension and reduce.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kVecThreads = 256;
+constexpr uint32_t kVecWaves = kVecThreads / 64;
+constexpr uint32_t kVecHeads = 8;      // query heads per workgroup
+constexpr uint32_t kVecDvTile = 256;   // value dims per workgroup
+constexpr uint32_t kVecDvPerLane = kVecDvTile / 64;
+
+template <typename QE, typename CE>
+__global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a) {
+  using QT = typename QE::T;
+  using CT = typename CE::T;
+  const uint32_t bid = blockIdx.x;
+  const uint32_t part = bid % a.parts;
+  const uint32_t rest = bid / a.parts;
+  uint32_t y = rest % a.grid_y;
+  const uint32_t seq = rest / a.grid_y;
+  const uint32_t n_dvt = (a.value_head_size + kVecDvTile - 1) / kVecDvTile;
+  const uint32_t dvt = y % n_dvt;
+  y /= n_dvt;
+  const uint32_t n_hc = (a.group + kVecHeads - 1) / kVecHeads;
+  const uint32_t hc = y % n_hc;
+  const uint32_t kvh = y / n_hc;
+
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const uint32_t p0 = part * a.partition_tokens;
+  if (p0 >= len) return;  // uniform: no partition state is produced
+  const uint32_t p1 = min(p0 + a.partition_tokens, len);
+
+  const uint32_t heads = min(kVecHeads, a.group - hc * kVecHeads);
+  const uint32_t qh0 = kvh * a.group + hc * kVecHeads;
+  const uint32_t lane = threadIdx.x & 63U;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t D = a.head_size;
+  const uint32_t Dv = a.value_head_size;
+
+  float k_scale = 1.0f, v_scale = 1.0f;
+  if (a.key_scales != nullptr) {
+    k_scale = a.key_scales[kvh * a.scale_stride];
+    v_scale = a.value_scales[kvh * a.scale_stride];
+  }
+  const float sl2 = a.score_scale_log2 * k_scale;
+
+  const QT* q = static_cast<const QT*>(a.query) +
+                (static_cast<uint64_t>(seq) * a.query_heads + qh0) * D;
+  const CT* kc = static_cast<const CT*>(a.key_cache);
+  const CT* vc = static_cast<const CT*>(a.value_cache);
+  const int32_t* table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
+
+  float m[kVecHeads], l[kVecHeads], o[kVecHeads][kVecDvPerLane];
+#pragma unroll
+  for (uint32_t h = 0; h < kVecHeads; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < kVecDvPerLane; ++j) o[h][j] = 0.0f;
+  }
+
+  for (uint32_t t = p0 + wave; t < p1; t += kVecWaves) {
+    const uint32_t page = t % a.block_size;
+    const uint64_t blk = static_cast<uint64_t>(table[t / a.block_size]);
+    const uint64_t krow = blk * a.k_block + page * a.k_page + kvh * a.k_head;
+    const uint64_t vrow = blk * a.v_block + page * a.v_page + kvh * a.v_head;
+    float acc[kVecHeads];
+#pragma unroll
+    for (uint32_t h = 0; h < kVecHeads; ++h) acc[h] = 0.0f;
+    for (uint32_t d = lane; d < D; d += 64) {
+      const float kv = CE::to_f(kc[krow + d]);
+#pragma unroll
+      for (uint32_t h = 0; h < kVecHeads; ++h) {
+        if (h < heads) acc[h] = fmaf(QE::to_f(q[h * D + d]), kv, acc[h]);
+      }
+    }
+    float vv[kVecDvPerLane];
+#pragma unroll
+    for (uint32_t j = 0; j < kVecDvPerLane; ++j) {
+      const uint32_t d = dvt * kVecDvTile + j * 64 + lane;
+      vv[j] = d < Dv ? CE::to_f(vc[vrow + d]) * v_scale : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t h = 0; h < kVecHeads; ++h) {
+      if (h < heads) {
+        const float s = wave_sum(acc[h]) * sl2;
+        const float mn = fmaxf(m[h], s);
+        const float alpha = exp2f(m[h] - mn);
+        const float p = exp2f(s - mn);
+        l[h] = fmaf(l[h], alpha, p);
+#pragma unroll
+        for (uint32_t j = 0; j < kVecDvPerLane; ++j) o[h][j] = fmaf(o[h][j], alpha, p * vv[j]);
+        m[h] = mn;
+      }
+    }
+  }
+
+  __shared__ float sm_m[kVecWaves][kVecHeads];
+  __shared__ float sm_l[kVecWaves][kVecHeads];
+  __shared__ float sm_o[kVecWaves][kVecHeads][kVecDvTile];
+  if (lane == 0) {
+#pragma unroll
+    for (uint32_t h = 0; h < kVecHeads; ++h) {
+      sm_m[wave][h] = m[h];
+      sm_l[wave][h] = l[h];
+    }
+  }
+#pragma unroll
+  for (uint32_t h = 0; h < kVecHeads; ++h) {
+#pragma unroll
+    for (uint32_t j = 0; j < kVecDvPerLane; ++j) sm_o[wave][h][j * 64 + lane] = o[h][j];
+  }
+  __syncthreads();
+
+  for (uint32_t idx = threadIdx.x; idx < kVecHeads * kVecDvTile; idx += kVecThreads) {
+    const uint32_t h = idx / kVecDvTile;
+    const uint32_t dd = idx % kVecDvTile;
+    const uint32_t d = dvt * kVecDvTile + dd;
+    if (h >= heads || d >= Dv) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t w = 0; w < kVecWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < kVecWaves; ++w) {
+      const float f = exp2f(sm_m[w][h] - M);  // 0 for a wave that saw no token
+      L = fmaf(sm_l[w][h], f, L);
+      O = fmaf(sm_o[w][h][dd], f, O);
+    }
+    const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + qh0 + h;
+    if (a.parts == 1) {
+      static_cast<QT*>(a.output)[row * Dv + d] = QE::from_f(O / L);
+      if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
+    } else {
+      const uint64_t state = row * a.parts + part;
+      a.ws_o[state * Dv + d] = O;
+      if (d == 0) {
+        a.ws_ml[state * 2] = M;
+        a.ws_ml[state * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Matrix-core kernel.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kChunk = 32;        // tokens per wave iteration
+constexpr uint32_t kDim = 128;         // head_size == value_head_size
+constexpr uint32_t kTileRowBytes = kDim * 2;
+constexpr uint32_t kTileBytes = kChunk * kTileRowBytes;  // 8 KiB V tile per wave
+
+template <typename QE>
+struct MfmaOps;
+
+template <>
+struct MfmaOps<Bf16Elem> {
+  using vec8 = bf16x8;
+  static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // Eight FP8 E4M3FN bytes (two dwords) to eight 16-bit values, exactly.
+  static __device__ __forceinline__ vec8 from_fp8(uint32_t lo, uint32_t hi) {
+    const bf16x2 a0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const bf16x2 a1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const bf16x2 a2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const bf16x2 a3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+    return vec8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    const bf16x2 v{static_cast<__bf16>(x), static_cast<__bf16>(y)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+template <>
+struct MfmaOps<F16Elem> {
+  using vec8 = f16x8;
+  static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ vec8 from_fp8(uint32_t lo, uint32_t hi) {
+    const f16x2 a0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
+    const f16x2 a1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
+    const f16x2 a2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
+    const f16x2 a3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
+    return vec8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    const f16x2 v{static_cast<_Float16>(x), static_cast<_Float16>(y)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// Loads of one 32-token chunk held in registers.
+//   16-bit caches: k[sb][kc] = 8 dims of token sb*16 + (lane & 15) at dims
+//   kc*32 + (lane >> 4)*8; v[i] = 8 dims (lane & 15)*8 of token
+//   4*i + (lane >> 4).
+//   FP8 caches: k[sb][j] = 16 bytes of token sb*16 + (lane & 15) at dims
+//   j*64 + (lane >> 4)*16; v[i] = 16 bytes (lane & 7)*16 of token
+//   8*i + (lane >> 3).
+template <bool kFp8>
+struct ChunkRegs {
+  static constexpr int kKLoads = kFp8 ? 2 : 4;
+  static constexpr int kVLoads = kFp8 ? 4 : 8;
+  u32x4 k[2][kKLoads];
+  u32x4 v[kVLoads];
+};
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *static_cast<const u32x4*>(p);
+}
+
+template <typename QE, bool kFp8, int kHeadTiles>
+struct MfmaDecoder {
+  using Ops = MfmaOps<QE>;
+  using vec8 = typename Ops::vec8;
+  using CT = typename std::conditional<kFp8, uint8_t, uint16_t>::type;
+  static constexpr uint32_t kElem = kFp8 ? 1 : 2;
+
+  const DecodeArgs& a;
+  uint32_t lane, g, c, seq, kvh, p0, p1;
+  const int32_t* table;
+  const CT* kbase;  // key cache + kv_head offset
+  const CT* vbase;
+  uint8_t* tile;  // this wave's LDS V tile
+  float sl2;
+
+  vec8 qb[kHeadTiles][4];
+  f32x4 acc[kHeadTiles][8];  // O^T tiles: dims dt*16 + 4g + r, head c
+  float m[kHeadTiles];       // running max (log2 units) of head c
+  float lsum[kHeadTiles];    // partial denominator over this lane's tokens
+
+  __device__ __forceinline__ MfmaDecoder(const DecodeArgs& args) : a(args) {}
+
+  // Logical-block IDs for the chunk starting at c0: lane i holds the table
+  // entry of logical block (c0 >> shift) + i, for the blocks the chunk's
+  // clamped tokens touch.
+  __device__ __forceinline__ int32_t fetch_ids(uint32_t c0) const {
+    const uint32_t lb0 = c0 >> a.block_shift;
+    const uint32_t last = (min(c0 + kChunk, p1) - 1U) >> a.block_shift;
+    int32_t id = 0;
+    if (lb0 + lane <= last) id = table[lb0 + lane];
+    return id;
+  }
+
+  // Element offset of the row of token t (clamped into the partition).
+  __device__ __forceinline__ void row_of(uint32_t c0, int32_t ids, uint32_t t, uint64_t stride_b,
+                                         uint64_t stride_p, uint64_t* off) const {
+    t = min(t, p1 - 1U);
+    const uint32_t src = (t >> a.block_shift) - (c0 >> a.block_shift);
+    const uint32_t blk = static_cast<uint32_t>(__shfl(ids, static_cast<int>(src), 64));
+    const uint32_t page = t & (a.block_size - 1U);
+    *off = static_cast<uint64_t>(blk) * stride_b + static_cast<uint64_t>(page) * stride_p;
+  }
+
+  __device__ __forceinline__ void issue(ChunkRegs<kFp8>& r, int32_t ids, uint32_t c0) const {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      uint64_t off;
+      row_of(c0, ids, c0 + sb * 16 + c, a.k_block, a.k_page, &off);
+      const CT* p = kbase + off;
+#pragma unroll
+      for (int j = 0; j < ChunkRegs<kFp8>::kKLoads; ++j) {
+        const uint32_t dim = kFp8 ? (j * 64 + g * 16) : (j * 32 + g * 8);
+        r.k[sb][j] = load16(p + dim);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < ChunkRegs<kFp8>::kVLoads; ++i) {
+      const uint32_t t = kFp8 ? (c0 + 8 * i + (lane >> 3)) : (c0 + 4 * i + (lane >> 4));
+      uint64_t off;
+      row_of(c0, ids, t, a.v_block, a.v_page, &off);
+      const uint32_t dim = kFp8 ? (lane & 7U) * 16 : (lane & 15U) * 8;
+      r.v[i] = load16(vbase + off + dim);
+    }
+  }
+
+  // LDS V tile: 32 rows of 128 16-bit values; the 16-byte chunk ch of row t
+  // is stored at chunk ch ^ (2 * ((t >> 2) & 3)) so that the transposed
+  // reads below (four token rows 4 apart, 16 consecutive dims) hit 32
+  // distinct banks.
+  static __device__ __forceinline__ uint32_t tile_off(uint32_t t, uint32_t ch) {
+    return t * kTileRowBytes + ((ch ^ (((t >> 2) & 3U) << 1)) << 4);
+  }
+
+  __device__ __forceinline__ void stage_v(const ChunkRegs<kFp8>& r) const {
+#pragma unroll
+    for (int i = 0; i < ChunkRegs<kFp8>::kVLoads; ++i) {
+      if (kFp8) {
+        const uint32_t t = 8 * i + (lane >> 3);
+        const uint32_t ch = (lane & 7U) * 2;
+        const vec8 lo = Ops::from_fp8(r.v[i][0], r.v[i][1]);
+        const vec8 hi = Ops::from_fp8(r.v[i][2], r.v[i][3]);
+        *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = lo;
+        *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = hi;
+      } else {
+        const uint32_t t = 4 * i + (lane >> 4);
+        const uint32_t ch = lane & 15U;
+        *reinterpret_cast<u32x4*>(tile + tile_off(t, ch)) = r.v[i];
+      }
+    }
+  }
+
+  __device__ __forceinline__ vec8 k_operand(const ChunkRegs<kFp8>& r, int sb, int kc) const {
+    if (kFp8) {
+      const u32x4 w = r.k[sb][kc >> 1];
+      return (kc & 1) ? Ops::from_fp8(w[2], w[3]) : Ops::from_fp8(w[0], w[1]);
+    } else {
+      return __builtin_bit_cast(vec8, r.k[sb][kc]);
+    }
+  }
+
+  // PV A operand: V^T[dims dt*16 + c][8 token slots of lane group g]; slot j
+  // of group g is token (j >> 2) * 16 + 4g + (j & 3), the token whose
+  // probability the QK output placed in this lane.
+  __device__ __forceinline__ vec8 v_operand(uint32_t dt) const {
+    const uint32_t d = dt * 16 + c;
+    const uint32_t ch = d >> 3;
+    const uint32_t e = (d & 7U) * 2;
+    uint16_t x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t t = (j >> 2) * 16 + 4 * g + (j & 3);
+      x[j] = *reinterpret_cast<const uint16_t*>(tile + tile_off(t, ch) + e);
+    }
+    u32x4 w;
+    w[0] = x[0] | (static_cast<uint32_t>(x[1]) << 16);
+    w[1] = x[2] | (static_cast<uint32_t>(x[3]) << 16);
+    w[2] = x[4] | (static_cast<uint32_t>(x[5]) << 16);
+    w[3] = x[6] | (static_cast<uint32_t>(x[7]) << 16);
+    return __builtin_bit_cast(vec8, w);
+  }
+
+  // Second half of a chunk: QK^T, online softmax and PV. The chunk's V has
+  // already been staged into the LDS tile.
+  __device__ __forceinline__ void compute(const ChunkRegs<kFp8>& r, uint32_t c0) {
+
+    // S[token 4g + r][head c] for the two 16-token halves of the chunk.
+    f32x4 s[kHeadTiles][2];
+#pragma unroll
+    for (int ht = 0; ht < kHeadTiles; ++ht) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) z = Ops::mma(k_operand(r, sb, kc), qb[ht][kc], z);
+        s[ht][sb] = z;
+      }
+    }
+
+    vec8 pb[kHeadTiles];
+#pragma unroll
+    for (int ht = 0; ht < kHeadTiles; ++ht) {
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const uint32_t t = c0 + sb * 16 + 4 * g + rr;
+          const float v = t < p1 ? s[ht][sb][rr] * sl2 : -INFINITY;
+          s[ht][sb][rr] = v;
+          cmax = fmaxf(cmax, v);
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      const float mn = fmaxf(m[ht], cmax);  // finite: every chunk has a valid token
+      const float alpha = __builtin_amdgcn_exp2f(m[ht] - mn);
+      m[ht] = mn;
+      float p[8];
+      float psum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(s[ht][j >> 2][j & 3] - mn);
+        psum += p[j];
+      }
+      lsum[ht] = fmaf(lsum[ht], alpha, psum);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[ht][dt] *= alpha;
+      u32x4 w;
+      w[0] = Ops::pack2(p[0], p[1]);
+      w[1] = Ops::pack2(p[2], p[3]);
+      w[2] = Ops::pack2(p[4], p[5]);
+      w[3] = Ops::pack2(p[6], p[7]);
+      pb[ht] = __builtin_bit_cast(vec8, w);
+    }
+
+#pragma unroll
+    for (uint32_t dt = 0; dt < 8; ++dt) {
+      const vec8 va = v_operand(dt);
+#pragma unroll
+      for (int ht = 0; ht < kHeadTiles; ++ht) acc[ht][dt] = Ops::mma(va, pb[ht], acc[ht][dt]);
+    }
+    wave_fence_lds();
+  }
+};
+
+template <typename QE, bool kFp8, int kHeadTiles>
+__global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kernel(DecodeArgs a) {
+  using Dec = MfmaDecoder<QE, kFp8, kHeadTiles>;
+  using vec8 = typename Dec::vec8;
+  using CT = typename Dec::CT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const uint32_t bid = blockIdx.x;
+  const uint32_t part = bid % a.parts;
+  const uint32_t rest = bid / a.parts;
+  const uint32_t kvh = rest % a.kv_heads;
+  const uint32_t seq = rest / a.kv_heads;
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const uint32_t p0 = part * a.partition_tokens;
+  if (p0 >= len) return;  // uniform across the workgroup
+
+  Dec dec(a);
+  dec.lane = threadIdx.x & 63U;
+  dec.g = dec.lane >> 4;
+  dec.c = dec.lane & 15U;
+  dec.seq = seq;
+  dec.kvh = kvh;
+  dec.p0 = p0;
+  dec.p1 = min(p0 + a.partition_tokens, len);
+  dec.table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
+  dec.kbase = static_cast<const CT*>(a.key_cache) + static_cast<uint64_t>(kvh) * a.k_head;
+  dec.vbase = static_cast<const CT*>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t waves = blockDim.x >> 6;
+  const uint32_t state_bytes = kHeadTiles * 16 * (kDim + 2) * 4;
+  const uint32_t wave_bytes = state_bytes > kTileBytes ? state_bytes : kTileBytes;
+  dec.tile = smem + wave * wave_bytes;
+
+  float k_scale = 1.0f, v_scale = 1.0f;
+  if (kFp8) {
+    k_scale = a.key_scales[kvh * a.scale_stride];
+    v_scale = a.value_scales[kvh * a.scale_stride];
+  }
+  dec.sl2 = a.score_scale_log2 * k_scale;
+
+  // Query operand: head ht*16 + c, the dims paired with this lane's K dims.
+  const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
+                         (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group) * kDim;
+#pragma unroll
+  for (int ht = 0; ht < kHeadTiles; ++ht) {
+    const uint32_t h = ht * 16 + dec.c;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
+      u32x4 w = {0U, 0U, 0U, 0U};
+      if (h < a.group) w = load16(qrow + h * kDim + dim);
+      dec.qb[ht][kc] = __builtin_bit_cast(vec8, w);
+    }
+    dec.m[ht] = -INFINITY;
+    dec.lsum[ht] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) dec.acc[ht][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // Chunks of this partition: chunk k covers [p0 + 32k, p0 + 32k + 32); wave
+  // w takes chunks w, w + waves, ...
+  const uint32_t nck = (dec.p1 - p0 + kChunk - 1) / kChunk;
+  const uint32_t my_n = nck > wave ? (nck - wave + waves - 1) / waves : 0;
+  const uint32_t stride_tokens = waves * kChunk;
+  uint32_t cA = p0 + wave * kChunk;
+  if (my_n > 0) {
+    // Two register buffers in ping-pong. Per step: fetch block IDs two
+    // chunks ahead, stage the current chunk's V into LDS (freeing its
+    // registers), issue the next chunk's K/V loads, then compute the current
+    // chunk while those loads are in flight.
+    ChunkRegs<kFp8> bufA, bufB;
+    int32_t idsA = dec.fetch_ids(cA);
+    int32_t idsB = my_n > 1 ? dec.fetch_ids(cA + stride_tokens) : 0;
+    dec.issue(bufA, idsA, cA);
+    for (uint32_t i = 0; i < my_n; i += 2) {
+      const uint32_t cB = cA + stride_tokens;
+      if (i + 2 < my_n) idsA = dec.fetch_ids(cB + stride_tokens);
+      dec.stage_v(bufA);
+      wave_fence_lds();
+      if (i + 1 < my_n) dec.issue(bufB, idsB, cB);
+      dec.compute(bufA, cA);
+      if (i + 1 >= my_n) break;
+      const uint32_t cC = cB + stride_tokens;
+      if (i + 3 < my_n) idsB = dec.fetch_ids(cC + stride_tokens);
+      dec.stage_v(bufB);
+      wave_fence_lds();
+      if (i + 2 < my_n) dec.issue(bufA, idsA, cC);
+      dec.compute(bufB, cB);
+      cA = cC;
+    }
+  }
+
+  // Per-lane partial denominators -> per head (sum over the 4 lane groups).
+#pragma unroll
+  for (int ht = 0; ht < kHeadTiles; ++ht) {
+    float l = dec.lsum[ht];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    dec.lsum[ht] = l;
+  }
+
+  // Workgroup reduction: each wave publishes (m, l, O[h][d]) in its LDS slot.
+  float* st = reinterpret_cast<float*>(dec.tile);
+  __syncthreads();  // every wave is done with its V tile
+#pragma unroll
+  for (int ht = 0; ht < kHeadTiles; ++ht) {
+    const uint32_t h = ht * 16 + dec.c;
+    float* hs = st + h * (kDim + 2);
+    if (dec.g == 0) {
+      hs[0] = dec.m[ht];
+      hs[1] = dec.lsum[ht];
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) hs[2 + dt * 16 + 4 * dec.g + rr] = dec.acc[ht][dt][rr];
+    }
+  }
+  __syncthreads();
+
+  const uint32_t heads = min(a.group, static_cast<uint32_t>(kHeadTiles * 16));
+  for (uint32_t idx = threadIdx.x; idx < heads * kDim; idx += blockDim.x) {
+    const uint32_t h = idx / kDim;
+    const uint32_t d = idx % kDim;
+    float M = -INFINITY;
+    for (uint32_t w = 0; w < waves; ++w) {
+      const float* hs = reinterpret_cast<const float*>(smem + w * wave_bytes) + h * (kDim + 2);
+      M = fmaxf(M, hs[0]);
+    }
+    float L = 0.0f, O = 0.0f;
+    for (uint32_t w = 0; w < waves; ++w) {
+      const float* hs = reinterpret_cast<const float*>(smem + w * wave_bytes) + h * (kDim + 2);
+      const float f = exp2f(hs[0] - M);  // 0 for a wave that had no chunk
+      L = fmaf(hs[1], f, L);
+      O = fmaf(hs[2 + d], f, O);
+    }
+    O *= v_scale;
+    const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h;
+    if (a.parts == 1) {
+      static_cast<uint16_t*>(a.output)[row * kDim + d] = QE::from_f(O / L);
+      if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
+    } else {
+      const uint64_t state = row * a.parts + part;
+      a.ws_o[state * kDim + d] = O;
+      if (d == 0) {
+        a.ws_ml[state * 2] = M;
+        a.ws_ml[state * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K merge: one workgroup per (sequence, query head) row. Only the
+// ceil(len / partition_tokens) partitions that hold tokens are read.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kMergeThreads = 128;
+constexpr uint32_t kMergeWindow = 512;
+
+template <typename QE>
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
+  using QT = typename QE::T;
+  __shared__ float factor[kMergeWindow];
+  __shared__ float red[kMergeThreads / 64];
+  const uint32_t row = blockIdx.x;
+  const uint32_t seq = row / a.query_heads;
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const uint32_t n = (len + a.partition_tokens - 1) / a.partition_tokens;
+  const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
+  const float* os = a.ws_o + static_cast<uint64_t>(row) * a.parts * a.value_head_size;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63U;
+  const uint32_t wave = tid >> 6;
+
+  float M = -INFINITY;
+  for (uint32_t p = tid; p < n; p += kMergeThreads) M = fmaxf(M, ml[2 * p]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = red[0];
+  for (uint32_t w = 1; w < kMergeThreads / 64; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+
+  float Lp = 0.0f;
+  for (uint32_t p = tid; p < n; p += kMergeThreads) Lp = fmaf(ml[2 * p + 1], exp2f(ml[2 * p] - M), Lp);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) Lp += __shfl_xor(Lp, off, 64);
+  if (lane == 0) red[wave] = Lp;
+  __syncthreads();
+  float L = 0.0f;
+  for (uint32_t w = 0; w < kMergeThreads / 64; ++w) L += red[w];
+  const float inv = 1.0f / L;
+
+  const uint32_t Dv = a.value_head_size;
+  for (uint32_t d0 = 0; d0 < Dv; d0 += kMergeThreads) {
+    const uint32_t d = d0 + tid;
+    float O = 0.0f;
+    for (uint32_t w0 = 0; w0 < n; w0 += kMergeWindow) {
+      const uint32_t wn = min(kMergeWindow, n - w0);
+      __syncthreads();
+      for (uint32_t p = tid; p < wn; p += kMergeThreads) factor[p] = exp2f(ml[2 * (w0 + p)] - M);
+      __syncthreads();
+      if (d < Dv) {
+        for (uint32_t p = 0; p < wn; ++p) {
+          O = fmaf(os[static_cast<uint64_t>(w0 + p) * Dv + d], factor[p], O);
+        }
+      }
+    }
+    if (d < Dv) static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * Dv + d] = QE::from_f(O * inv);
+  }
+  if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
+}
+
+// ---------------------------------------------------------------------------
+// Host side: error reporting, telemetry, validation, planning, launch.
+// ---------------------------------------------------------------------------
+thread_local std::string g_last_error;
+std::atomic<uint64_t> g_decode_launches{0};
+
+int fail(int status, const char* message) {
+  g_last_error = message;
+  return status;
+}
+
+struct TimingState {
+  std::mutex mu;
+  bool enabled = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[2];
+  double total_ms[2] = {0.0, 0.0};
+  uint64_t launches[2] = {0, 0};
+};
+
+TimingState& timing() {
+  static TimingState* state = new TimingState();
+  return *state;
+}
+
+struct TimedLaunch {
+  hipEvent_t start = nullptr, stop = nullptr;
+  int kernel;
+  hipStream_t stream;
+  TimedLaunch(int k, hipStream_t s) : kernel(k), stream(s) {
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    if (!t.enabled) return;
+    if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess) {
+      start = stop = nullptr;
+      return;
+    }
+    (void)hipEventRecord(start, stream);
+  }
+  ~TimedLaunch() {
+    if (start == nullptr) return;
+    (void)hipEventRecord(stop, stream);
+    TimingState& t = timing();
+    std::lock_guard<std::mutex> lock(t.mu);
+    t.pending[kernel].emplace_back(start, stop);
+  }
+};
+
+enum DTypeCode : uint32_t { kF32 = LOOM_HIP_F32, kF16 = LOOM_HIP_F16, kBf16 = LOOM_HIP_BF16 };
+
+struct Problem {
+  uint32_t dtype;
+  const void* query;
+  const void* key_cache;
+  const void* value_cache;
+  const float* key_scales;
+  const float* value_scales;
+  const int32_t* block_tables;
+  const int32_t* sequence_lengths;
+  void* output;
+  float* lse;
+  float* workspace;
+  uint64_t workspace_elements;
+  uint32_t sequences, query_heads, kv_heads, head_size, value_head_size;
+  uint32_t num_blocks, block_size, cache_encoding, scale_stride;
+  uint64_t k_block, k_page, k_head, v_block, v_page, v_head;
+  uint32_t max_blocks_per_sequence, max_sequence_length;
+  uint32_t partition_tokens;  // 0 = one partition per sequence
+  float scale;
+};
+
+size_t elem_size(uint32_t dtype) { return dtype == kF32 ? 4 : 2; }
+
+size_t cache_elem_size(const Problem& p) {
+  return p.cache_encoding == LOOM_HIP_KV_CACHE_FP8_E4M3 ? 1 : elem_size(p.dtype);
+}
+
+bool mul_ok(uint64_t a, uint64_t b, uint64_t* out) {
+  if (a != 0 && b > std::numeric_limits<uint64_t>::max() / a) return false;
+  *out = a * b;
+  return true;
+}
+
+uint64_t parts_for(uint32_t max_len, uint32_t partition_tokens) {
+  if (partition_tokens == 0 || partition_tokens >= max_len) return 1;
+  return (static_cast<uint64_t>(max_len) + partition_tokens - 1) / partition_tokens;
+}
+
+bool is_pow2(uint32_t v) { return v != 0 && (v & (v - 1)) == 0; }
+
+// Byte span [lo, hi) of the elements a cache view can address.
+bool cache_span(const Problem& p, bool key, uint64_t* bytes) {
+  const uint64_t dim = key ? p.head_size : p.value_head_size;
+  const uint64_t sb = key ? p.k_block : p.v_block;
+  const uint64_t sp = key ? p.k_page : p.v_page;
+  const uint64_t sh = key ? p.k_head : p.v_head;
+  uint64_t a, b, c, total;
+  if (!mul_ok(p.num_blocks - 1ULL, sb, &a) || !mul_ok(p.block_size - 1ULL, sp, &b) ||
+      !mul_ok(p.kv_heads - 1ULL, sh, &c))
+    return false;
+  total = a + b;
+  if (total < a) return false;
+  if (total + c < total) return false;
+  total += c;
+  if (total + dim < total) return false;
+  total += dim;
+  return mul_ok(total, cache_elem_size(p), bytes);
+}
+
+bool overlaps(const void* a, uint64_t abytes, const void* b, uint64_t bbytes) {
+  if (a == nullptr || b == nullptr || abytes == 0 || bbytes == 0) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+// Host validation (paged_decode_attention.cu:999-1049 without the 1024
+// context cap, plus the extension fields). Returns LOOM_HIP_SUCCESS or the
+// status to report, with the thread-local message set.
+int validate(const Problem& p) {
+  if (p.dtype != kF32 && p.dtype != kF16 && p.dtype != kBf16)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown dtype code");
+  if (p.query == nullptr || p.key_cache == nullptr || p.value_cache == nullptr ||
+      p.block_tables == nullptr || p.sequence_lengths == nullptr || p.output == nullptr)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "paged decode pointers must be non-null");
+  if (p.sequences == 0 || p.query_heads == 0 || p.kv_heads == 0 || p.head_size == 0 ||
+      p.value_head_size == 0 || p.num_blocks == 0 || p.block_size == 0 ||
+      p.max_blocks_per_sequence == 0 || p.max_sequence_length == 0)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "paged decode dimensions must be non-zero");
+  if (p.query_heads % p.kv_heads != 0)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "query head count must be divisible by KV head count");
+  if (!std::isfinite(p.scale) || p.scale <= 0.0f)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "attention scale must be finite and positive");
+  if (static_cast<uint64_t>(p.max_sequence_length) >
+      static_cast<uint64_t>(p.block_size) * p.max_blocks_per_sequence)
+    return fail(LOOM_HIP_INVALID_ARGUMENT,
+                "maximum sequence length exceeds block-table capacity");
+  uint64_t tmp;
+  if (!mul_ok(static_cast<uint64_t>(p.sequences) * p.query_heads, p.head_size, &tmp) ||
+      !mul_ok(static_cast<uint64_t>(p.sequences) * p.query_heads, p.value_head_size, &tmp) ||
+      !mul_ok(static_cast<uint64_t>(p.num_blocks) * p.block_size, static_cast<uint64_t>(p.kv_heads) * p.head_size, &tmp) ||
+      !mul_ok(static_cast<uint64_t>(p.num_blocks) * p.block_size, static_cast<uint64_t>(p.kv_heads) * p.value_head_size, &tmp))
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "paged decode element count overflows");
+  if (static_cast<uint64_t>(p.sequences) * p.query_heads >
+      static_cast<uint64_t>(std::numeric_limits<int>::max()))
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "sequences * query_heads exceeds the launch grid");
+  if (p.cache_encoding != LOOM_HIP_KV_CACHE_NATIVE && p.cache_encoding != LOOM_HIP_KV_CACHE_FP8_E4M3)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown K/V cache encoding");
+  if (p.cache_encoding == LOOM_HIP_KV_CACHE_FP8_E4M3) {
+    if (p.key_scales == nullptr || p.value_scales == nullptr)
+      return fail(LOOM_HIP_INVALID_ARGUMENT, "FP8 K/V caches require key and value scales");
+    if (p.scale_stride > 1)
+      return fail(LOOM_HIP_INVALID_ARGUMENT, "scale_stride must be 0 (per tensor) or 1 (per KV head)");
+  } else if (p.key_scales != nullptr || p.value_scales != nullptr || p.scale_stride != 0) {
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "native K/V caches take no scales");
+  }
+  if (p.k_block == 0 || p.k_page == 0 || p.k_head == 0 || p.v_block == 0 || p.v_page == 0 ||
+      p.v_head == 0)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "cache strides must be non-zero");
+  uint64_t kbytes, vbytes;
+  if (!cache_span(p, true, &kbytes) || !cache_span(p, false, &vbytes))
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "cache strides overflow the address space");
+
+  const uint64_t parts = parts_for(p.max_sequence_length, p.partition_tokens);
+  uint64_t need = 0;
+  if (parts > 1) {
+    need = static_cast<uint64_t>(p.sequences) * p.query_heads * parts * (p.value_head_size + 2ULL);
+  }
+  if (need == 0) {
+    if (p.workspace != nullptr || p.workspace_elements != 0)
+      return fail(LOOM_HIP_INVALID_ARGUMENT,
+                  "this shape uses a single partition; the workspace must be null with zero elements");
+  } else if (p.workspace == nullptr || p.workspace_elements < need) {
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "split-K workspace is missing or too small");
+  }
+
+  // Output, LSE and workspace must not alias any input or each other
+  // (the byte-range rule of the reference bridge, cuda/mod.rs:119-153).
+  const uint64_t qbytes = static_cast<uint64_t>(p.sequences) * p.query_heads * p.head_size * elem_size(p.dtype);
+  const uint64_t obytes = static_cast<uint64_t>(p.sequences) * p.query_heads * p.value_head_size * elem_size(p.dtype);
+  const uint64_t tbytes = static_cast<uint64_t>(p.sequences) * p.max_blocks_per_sequence * 4;
+  const uint64_t lbytes = static_cast<uint64_t>(p.sequences) * 4;
+  const uint64_t lsebytes = p.lse ? static_cast<uint64_t>(p.sequences) * p.query_heads * 4 : 0;
+  const uint64_t wbytes = p.workspace ? p.workspace_elements * 4 : 0;
+  const uint64_t sbytes = p.scale_stride ? static_cast<uint64_t>(p.kv_heads) * 4 : 4;
+  struct Region { const void* ptr; uint64_t bytes; };
+  const Region inputs[] = {
+      {p.query, qbytes}, {p.key_cache, kbytes}, {p.value_cache, vbytes},
+      {p.block_tables, tbytes}, {p.sequence_lengths, lbytes},
+      {p.key_scales, p.key_scales ? sbytes : 0}, {p.value_scales, p.value_scales ? sbytes : 0}};
+  const Region outputs[] = {{p.output, obytes}, {p.lse, lsebytes}, {p.workspace, wbytes}};
+  for (const Region& o : outputs) {
+    for (const Region& i : inputs) {
+      if (overlaps(o.ptr, o.bytes, i.ptr, i.bytes))
+        return fail(LOOM_HIP_INVALID_ARGUMENT, "output, LSE and workspace must not overlap the inputs");
+    }
+  }
+  for (int i = 0; i < 3; ++i) {
+    for (int j = i + 1; j < 3; ++j) {
+      if (overlaps(outputs[i].ptr, outputs[i].bytes, outputs[j].ptr, outputs[j].bytes))
+        return fail(LOOM_HIP_INVALID_ARGUMENT, "output, LSE and workspace must not overlap each other");
+    }
+  }
+  return LOOM_HIP_SUCCESS;
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
+
+// Shape-level eligibility of the matrix-core kernel.
+bool mfma_shape(uint32_t dtype, uint32_t head_size, uint32_t value_head_size,
+                uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
+  return (dtype == kF16 || dtype == kBf16) && head_size == kDim && value_head_size == kDim &&
+         query_heads / kv_heads <= 32 && is_pow2(block_size);
+}
+
+bool mfma_eligible(const Problem& p) {
+  if (!mfma_shape(p.dtype, p.head_size, p.value_head_size, p.query_heads, p.kv_heads, p.block_size))
+    return false;
+  const uint64_t es = cache_elem_size(p);
+  const uint64_t strides[] = {p.k_block, p.k_page, p.k_head, p.v_block, p.v_page, p.v_head};
+  for (uint64_t s : strides) {
+    if ((s * es) % 16 != 0) return false;
+  }
+  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache);
+}
+
+uint32_t log2u(uint32_t v) {
+  uint32_t r = 0;
+  while ((1U << r) < v) ++r;
+  return r;
+}
+
+template <typename QE>
+int launch_merge(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
+  TimedLaunch timed(LOOM_HIP_KERNEL_MERGE, stream);
+  hipLaunchKernelGGL(merge_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
+template <typename QE, bool kFp8, int kHT>
+int launch_mfma(const DecodeArgs& args, uint64_t grid, uint32_t waves, hipStream_t stream) {
+  const uint32_t state_bytes = kHT * 16 * (kDim + 2) * 4;
+  const uint32_t wave_bytes = state_bytes > kTileBytes ? state_bytes : kTileBytes;
+  const size_t shared = static_cast<size_t>(waves) * wave_bytes;
+  TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  hipLaunchKernelGGL((decode_mfma_kernel<QE, kFp8, kHT>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(waves * 64), shared, stream, args);
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
+template <typename QE, typename CE>
+int launch_vector(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
+  TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  hipLaunchKernelGGL((decode_vector_kernel<QE, CE>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(kVecThreads), 0, stream, args);
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
+template <typename QE>
+int run_typed(const Problem& p, hipStream_t stream) {
+  const uint64_t parts = parts_for(p.max_sequence_length, p.partition_tokens);
+  const uint32_t partition_tokens = parts > 1 ? p.partition_tokens : p.max_sequence_length;
+  const uint32_t group = p.query_heads / p.kv_heads;
+  const bool fp8 = p.cache_encoding == LOOM_HIP_KV_CACHE_FP8_E4M3;
+
+  DecodeArgs args{};
+  args.query = p.query;
+  args.key_cache = p.key_cache;
+  args.value_cache = p.value_cache;
+  args.key_scales = fp8 ? p.key_scales : nullptr;
+  args.value_scales = fp8 ? p.value_scales : nullptr;
+  args.block_tables = p.block_tables;
+  args.sequence_lengths = p.sequence_lengths;
+  args.output = p.output;
+  args.lse = p.lse;
+  if (parts > 1) {
+    args.ws_ml = p.workspace;
+    args.ws_o = p.workspace + static_cast<uint64_t>(p.sequences) * p.query_heads * parts * 2;
+  }
+  args.k_block = p.k_block;
+  args.k_page = p.k_page;
+  args.k_head = p.k_head;
+  args.v_block = p.v_block;
+  args.v_page = p.v_page;
+  args.v_head = p.v_head;
+  args.query_heads = p.query_heads;
+  args.kv_heads = p.kv_heads;
+  args.group = group;
+  args.head_size = p.head_size;
+  args.value_head_size = p.value_head_size;
+  args.block_size = p.block_size;
+  args.block_shift = log2u(p.block_size);
+  args.max_blocks = p.max_blocks_per_sequence;
+  args.partition_tokens = partition_tokens;
+  args.parts = static_cast<uint32_t>(parts);
+  args.scale_stride = p.scale_stride;
+  args.score_scale_log2 = p.scale * kLog2e;
+
+  int status = LOOM_HIP_SUCCESS;
+  bool use_mfma = false;
+  if constexpr (!std::is_same<QE, F32Elem>::value) use_mfma = mfma_eligible(p);
+  if (use_mfma) {
+    if constexpr (!std::is_same<QE, F32Elem>::value) {
+    const uint64_t grid = parts * p.kv_heads * static_cast<uint64_t>(p.sequences);
+    if (grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
+      return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
+    args.grid_y = p.kv_heads;
+    const uint32_t chunks = (partition_tokens + kChunk - 1) / kChunk;
+    const int ht = group > 16 ? 2 : 1;
+    const uint32_t max_waves = ht == 1 ? 8 : 4;
+    uint32_t waves = (chunks + 3) / 4;
+    waves = waves < 1 ? 1 : (waves > max_waves ? max_waves : waves);
+    if (ht == 1) {
+      status = fp8 ? launch_mfma<QE, true, 1>(args, grid, waves, stream)
+                   : launch_mfma<QE, false, 1>(args, grid, waves, stream);
+    } else {
+      status = fp8 ? launch_mfma<QE, true, 2>(args, grid, waves, stream)
+                   : launch_mfma<QE, false, 2>(args, grid, waves, stream);
+    }
+    }
+  } else {
+    const uint64_t n_hc = (group + kVecHeads - 1) / kVecHeads;
+    const uint64_t n_dvt = (p.value_head_size + kVecDvTile - 1) / kVecDvTile;
+    const uint64_t gy = static_cast<uint64_t>(p.kv_heads) * n_hc * n_dvt;
+    const uint64_t grid = parts * gy * p.sequences;
+    if (gy > std::numeric_limits<uint32_t>::max() ||
+        grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
+      return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
+    args.grid_y = static_cast<uint32_t>(gy);
+    status = fp8 ? launch_vector<QE, Fp8Elem>(args, grid, stream)
+                 : launch_vector<QE, QE>(args, grid, stream);
+  }
+  if (status != LOOM_HIP_SUCCESS) return fail(status, "decode kernel launch failed");
+  if (parts > 1) {
+    status = launch_merge<QE>(args, p.sequences * p.query_heads, stream);
+    if (status != LOOM_HIP_SUCCESS) return fail(status, "merge kernel launch failed");
+  }
+  return LOOM_HIP_SUCCESS;
+}
+
+int device_available() {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    (void)hipGetLastError();
+    return fail(LOOM_HIP_UNAVAILABLE, "no HIP device is available");
+  }
+  return LOOM_HIP_SUCCESS;
+}
+
+int run(const Problem& p, void* stream) {
+  int status = validate(p);
+  if (status != LOOM_HIP_SUCCESS) return status;
+  status = device_available();
+  if (status != LOOM_HIP_SUCCESS) return status;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (p.dtype) {
+    case kF32: status = run_typed<F32Elem>(p, s); break;
+    case kF16: status = run_typed<F16Elem>(p, s); break;
+    default: status = run_typed<Bf16Elem>(p, s); break;
+  }
+  if (status == LOOM_HIP_SUCCESS) g_decode_launches.fetch_add(1, std::memory_order_relaxed);
+  return status;
+}
+
+// Split-K policy of the reference-compatible split entry points. The shape
+// splits when (sequence, KV head) work items alone cannot fill the 256 CUs
+// and the context is long enough: partitions of at least 512 tokens, sized
+// so that the grid reaches about 2048 workgroups.
+uint32_t split_k_partition_tokens(uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+                                  uint32_t head_size, uint32_t value_head_size,
+                                  uint32_t max_sequence_length) {
+  if (sequences == 0 || query_heads == 0 || kv_heads == 0 || head_size == 0 ||
+      value_head_size == 0 || max_sequence_length == 0 || query_heads % kv_heads != 0)
+    return 0;
+  const uint64_t work = static_cast<uint64_t>(sequences) * kv_heads;
+  if (work >= 1024 || max_sequence_length < 1024) return 0;
+  const uint64_t want_parts = (2048 + work - 1) / work;
+  uint64_t tokens = (max_sequence_length + want_parts - 1) / want_parts;
+  tokens = ((tokens + kChunk - 1) / kChunk) * kChunk;
+  if (tokens < 512) tokens = 512;
+  if (parts_for(max_sequence_length, static_cast<uint32_t>(tokens)) < 2) return 0;
+  return static_cast<uint32_t>(tokens);
+}
+
+Problem base_problem(uint32_t dtype, const void* query, const void* key_cache,
+                     const void* value_cache, const int32_t* block_tables,
+                     const int32_t* sequence_lengths, void* output, uint32_t sequences,
+                     uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+                     uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+                     uint64_t key_block_stride, uint64_t value_block_stride,
+                     uint32_t max_blocks_per_sequence, uint32_t max_sequence_length, float scale) {
+  Problem p{};
+  p.dtype = dtype;
+  p.query = query;
+  p.key_cache = key_cache;
+  p.value_cache = value_cache;
+  p.block_tables = block_tables;
+  p.sequence_lengths = sequence_lengths;
+  p.output = output;
+  p.sequences = sequences;
+  p.query_heads = query_heads;
+  p.kv_heads = kv_heads;
+  p.head_size = head_size;
+  p.value_head_size = value_head_size;
+  p.num_blocks = num_blocks;
+  p.block_size = block_size;
+  p.cache_encoding = LOOM_HIP_KV_CACHE_NATIVE;
+  p.k_block = key_block_stride;
+  p.k_page = static_cast<uint64_t>(kv_heads) * head_size;
+  p.k_head = head_size;
+  p.v_block = value_block_stride;
+  p.v_page = static_cast<uint64_t>(kv_heads) * value_head_size;
+  p.v_head = value_head_size;
+  p.max_blocks_per_sequence = max_blocks_per_sequence;
+  p.max_sequence_length = max_sequence_length;
+  p.scale = scale;
+  return p;
+}
+
+// The base ABI requires block strides of at least one dense NHD block
+// (paged_decode_attention.cu:1034-1049).
+int check_block_strides(const Problem& p) {
+  const uint64_t kb = static_cast<uint64_t>(p.block_size) * p.kv_heads * p.head_size;
+  const uint64_t vb = static_cast<uint64_t>(p.block_size) * p.kv_heads * p.value_head_size;
+  if (p.k_block < kb || p.v_block < vb)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "cache block stride is smaller than one dense NHD block");
+  return LOOM_HIP_SUCCESS;
+}
+
+int run_base(Problem p, void* stream) {
+  if (p.block_size != 0 && p.kv_heads != 0) {
+    int status = check_block_strides(p);
+    if (status != LOOM_HIP_SUCCESS) return status;
+  }
+  return run(p, stream);
+}
+
+int run_split_k(Problem p, float* workspace, uint64_t workspace_elements, void* stream) {
+  const uint32_t tokens = split_k_partition_tokens(p.sequences, p.query_heads, p.kv_heads,
+                                                   p.head_size, p.value_head_size,
+                                                   p.max_sequence_length);
+  if (tokens == 0)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "paged decode shape does not select the split-K path");
+  if (workspace == nullptr)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "split-K workspace must be non-null");
+  p.partition_tokens = tokens;
+  p.workspace = workspace;
+  p.workspace_elements = workspace_elements;
+  if (p.block_size != 0 && p.kv_heads != 0) {
+    int status = check_block_strides(p);
+    if (status != LOOM_HIP_SUCCESS) return status;
+  }
+  return run(p, stream);
+}
+
+Problem extended_problem(uint32_t dtype, const void* query, const void* key_cache,
+                         const void* value_cache, const float* key_scales,
+                         const float* value_scales, const int32_t* block_tables,
+                         const int32_t* sequence_lengths, void* output, float* lse,
+                         float* workspace, uint64_t workspace_elements, uint32_t sequences,
+                         uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+                         uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+                         uint32_t cache_encoding, uint32_t scale_stride, uint64_t kb, uint64_t kp,
+                         uint64_t kh, uint64_t vb, uint64_t vp, uint64_t vh,
+                         uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+                         uint32_t partition_tokens, float scale) {
+  Problem p{};
+  p.dtype = dtype;
+  p.query = query;
+  p.key_cache = key_cache;
+  p.value_cache = value_cache;
+  p.key_scales = key_scales;
+  p.value_scales = value_scales;
+  p.block_tables = block_tables;
+  p.sequence_lengths = sequence_lengths;
+  p.output = output;
+  p.lse = lse;
+  p.workspace = workspace;
+  p.workspace_elements = workspace_elements;
+  p.sequences = sequences;
+  p.query_heads = query_heads;
+  p.kv_heads = kv_heads;
+  p.head_size = head_size;
+  p.value_head_size = value_head_size;
+  p.num_blocks = num_blocks;
+  p.block_size = block_size;
+  p.cache_encoding = cache_encoding;
+  p.scale_stride = scale_stride;
+  p.k_block = kb;
+  p.k_page = kp;
+  p.k_head = kh;
+  p.v_block = vb;
+  p.v_page = vp;
+  p.v_head = vh;
+  p.max_blocks_per_sequence = max_blocks_per_sequence;
+  p.max_sequence_length = max_sequence_length;
+  p.partition_tokens = partition_tokens;
+  p.scale = scale;
+  return p;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* loom_hip_status_string(int status) {
+  switch (status) {
+    case LOOM_HIP_SUCCESS: return "success";
+    case LOOM_HIP_INVALID_ARGUMENT: return "invalid argument";
+    case LOOM_HIP_UNSUPPORTED: return "unsupported";
+    case LOOM_HIP_LAUNCH_ERROR: return "HIP launch error";
+    case LOOM_HIP_UNAVAILABLE: return "HIP unavailable";
+    default: return "unknown Loom HIP status";
+  }
+}
+
+const char* loom_hip_backend_name(void) { return "loom-hip"; }
+
+uint32_t loom_hip_abi_version(void) { return 1; }
+
+const char* loom_hip_last_error_message(void) { return g_last_error.c_str(); }
+
+int loom_hip_launch_count(uint32_t operation, uint64_t* count) {
+  if (operation != LOOM_HIP_PAGED_DECODE_ATTENTION || count == nullptr)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown operator id or null count");
+  *count = g_decode_launches.load(std::memory_order_relaxed);
+  return LOOM_HIP_SUCCESS;
+}
+
+int loom_hip_reset_launch_count(uint32_t operation) {
+  if (operation != LOOM_HIP_PAGED_DECODE_ATTENTION)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown operator id");
+  g_decode_launches.store(0, std::memory_order_relaxed);
+  return LOOM_HIP_SUCCESS;
+}
+
+int loom_hip_kernel_timing_enable(uint32_t enable) {
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  t.enabled = enable != 0;
+  for (int k = 0; k < 2; ++k) {
+    for (auto& e : t.pending[k]) {
+      (void)hipEventSynchronize(e.second);
+      (void)hipEventDestroy(e.first);
+      (void)hipEventDestroy(e.second);
+    }
+    t.pending[k].clear();
+    t.total_ms[k] = 0.0;
+    t.launches[k] = 0;
+  }
+  return LOOM_HIP_SUCCESS;
+}
+
+int loom_hip_kernel_timing_read(uint32_t kernel, double* total_ms, uint64_t* launches) {
+  if (kernel > 1 || total_ms == nullptr || launches == nullptr)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown kernel id or null output");
+  TimingState& t = timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  for (auto& e : t.pending[kernel]) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(e.second) == hipSuccess &&
+        hipEventElapsedTime(&ms, e.first, e.second) == hipSuccess) {
+      t.total_ms[kernel] += ms;
+      t.launches[kernel] += 1;
+    }
+    (void)hipEventDestroy(e.first);
+    (void)hipEventDestroy(e.second);
+  }
+  t.pending[kernel].clear();
+  *total_ms = t.total_ms[kernel];
+  *launches = t.launches[kernel];
+  return LOOM_HIP_SUCCESS;
+}
+
+int loom_hip_paged_decode_attention_supports(
+    uint32_t dtype, uint32_t cache_encoding, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+    float scale, const char** reason, const char** kernel_family) {
+  const char* why = "supported";
+  int status = LOOM_HIP_SUCCESS;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBf16) {
+    status = LOOM_HIP_UNSUPPORTED;
+    why = "HIP paged decode attention supports F32, FP16 and BF16 queries";
+  } else if (cache_encoding > LOOM_HIP_KV_CACHE_FP8_E4M3) {
+    status = LOOM_HIP_UNSUPPORTED;
+    why = "HIP paged decode attention supports native and FP8 E4M3 K/V caches";
+  } else if (sequences == 0 || query_heads == 0 || kv_heads == 0 || head_size == 0 ||
+             value_head_size == 0 || num_blocks == 0 || block_size == 0 ||
+             max_blocks_per_sequence == 0 || max_sequence_length == 0) {
+    status = LOOM_HIP_INVALID_ARGUMENT;
+    why = "paged decode dimensions must be non-zero";
+  } else if (query_heads % kv_heads != 0) {
+    status = LOOM_HIP_INVALID_ARGUMENT;
+    why = "query head count must be divisible by KV head count";
+  } else if (!std::isfinite(scale) || scale <= 0.0f) {
+    status = LOOM_HIP_INVALID_ARGUMENT;
+    why = "attention scale must be finite and positive";
+  } else if (static_cast<uint64_t>(max_sequence_length) >
+             static_cast<uint64_t>(block_size) * max_blocks_per_sequence) {
+    status = LOOM_HIP_INVALID_ARGUMENT;
+    why = "maximum sequence length exceeds block-table capacity";
+  } else if (static_cast<uint64_t>(sequences) * query_heads >
+             static_cast<uint64_t>(std::numeric_limits<int>::max())) {
+    status = LOOM_HIP_UNSUPPORTED;
+    why = "paged decode shape exceeds the HIP launch grid";
+  }
+  if (reason != nullptr) *reason = why;
+  if (kernel_family != nullptr) {
+    *kernel_family = status != LOOM_HIP_SUCCESS ? ""
+                     : mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
+                         ? "mfma"
+                         : "vector";
+  }
+  return status;
+}
+
+int loom_hip_paged_decode_attention_f32(
+    const float* query, const float* key_cache, const float* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths, float* output,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint64_t key_block_stride, uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream) {
+  return run_base(base_problem(kF32, query, key_cache, value_cache, block_tables,
+                               sequence_lengths, output, sequences, query_heads, kv_heads,
+                               head_size, value_head_size, num_blocks, block_size,
+                               key_block_stride, value_block_stride, max_blocks_per_sequence,
+                               max_sequence_length, scale),
+                  stream);
+}
+
+int loom_hip_paged_decode_attention_f16(
+    const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths, uint16_t* output,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint64_t key_block_stride, uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream) {
+  return run_base(base_problem(kF16, query, key_cache, value_cache, block_tables,
+                               sequence_lengths, output, sequences, query_heads, kv_heads,
+                               head_size, value_head_size, num_blocks, block_size,
+                               key_block_stride, value_block_stride, max_blocks_per_sequence,
+                               max_sequence_length, scale),
+                  stream);
+}
+
+int loom_hip_paged_decode_attention_bf16(
+    const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths, uint16_t* output,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint64_t key_block_stride, uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream) {
+  return run_base(base_problem(kBf16, query, key_cache, value_cache, block_tables,
+                               sequence_lengths, output, sequences, query_heads, kv_heads,
+                               head_size, value_head_size, num_blocks, block_size,
+                               key_block_stride, value_block_stride, max_blocks_per_sequence,
+                               max_sequence_length, scale),
+                  stream);
+}
+
+uint64_t loom_hip_paged_decode_attention_split_k_workspace_elements(
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t max_sequence_length) {
+  const uint32_t tokens = split_k_partition_tokens(sequences, query_heads, kv_heads, head_size,
+                                                   value_head_size, max_sequence_length);
+  if (tokens == 0) return 0;
+  return static_cast<uint64_t>(sequences) * query_heads * parts_for(max_sequence_length, tokens) *
+         (value_head_size + 2ULL);
+}
+
+int loom_hip_paged_decode_attention_split_k_f32(
+    const float* query, const float* key_cache, const float* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths, float* output,
+    float* workspace, uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint64_t key_block_stride, uint64_t value_block_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length, float scale,
+    void* stream) {
+  return run_split_k(base_problem(kF32, query, key_cache, value_cache, block_tables,
+                                  sequence_lengths, output, sequences, query_heads, kv_heads,
+                                  head_size, value_head_size, num_blocks, block_size,
+                                  key_block_stride, value_block_stride, max_blocks_per_sequence,
+                                  max_sequence_length, scale),
+                     workspace, workspace_elements, stream);
+}
+
+int loom_hip_paged_decode_attention_split_k_f16(
+    const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths, uint16_t* output,
+    float* workspace, uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint64_t key_block_stride, uint64_t value_block_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length, float scale,
+    void* stream) {
+  return run_split_k(base_problem(kF16, query, key_cache, value_cache, block_tables,
+                                  sequence_lengths, output, sequences, query_heads, kv_heads,
+                                  head_size, value_head_size, num_blocks, block_size,
+                                  key_block_stride, value_block_stride, max_blocks_per_sequence,
+                                  max_sequence_length, scale),
+                     workspace, workspace_elements, stream);
+}
+
+int loom_hip_paged_decode_attention_split_k_bf16(
+    const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths, uint16_t* output,
+    float* workspace, uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint64_t key_block_stride, uint64_t value_block_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length, float scale,
+    void* stream) {
+  return run_split_k(base_problem(kBf16, query, key_cache, value_cache, block_tables,
+                                  sequence_lengths, output, sequences, query_heads, kv_heads,
+                                  head_size, value_head_size, num_blocks, block_size,
+                                  key_block_stride, value_block_stride, max_blocks_per_sequence,
+                                  max_sequence_length, scale),
+                     workspace, workspace_elements, stream);
+}
+
+uint64_t loom_hip_paged_decode_attention_extended_workspace_elements(
+    uint32_t sequences, uint32_t query_heads, uint32_t value_head_size,
+    uint32_t max_sequence_length, uint32_t partition_tokens) {
+  if (max_sequence_length == 0) return 0;
+  const uint64_t parts = parts_for(max_sequence_length, partition_tokens);
+  if (parts <= 1) return 0;
+  return static_cast<uint64_t>(sequences) * query_heads * parts * (value_head_size + 2ULL);
+}
+
+int loom_hip_paged_decode_attention_extended_f32(
+    const float* query, const void* key_cache, const void* value_cache, const float* key_scales,
+    const float* value_scales, const int32_t* block_tables, const int32_t* sequence_lengths,
+    float* output, float* lse, float* workspace, uint64_t workspace_elements,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint32_t cache_encoding, uint32_t scale_stride, uint64_t key_block_stride,
+    uint64_t key_page_stride, uint64_t key_head_stride, uint64_t value_block_stride,
+    uint64_t value_page_stride, uint64_t value_head_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, uint32_t partition_tokens, float scale, void* stream) {
+  return run(extended_problem(kF32, query, key_cache, value_cache, key_scales, value_scales,
+                              block_tables, sequence_lengths, output, lse, workspace,
+                              workspace_elements, sequences, query_heads, kv_heads, head_size,
+                              value_head_size, num_blocks, block_size, cache_encoding,
+                              scale_stride, key_block_stride, key_page_stride, key_head_stride,
+                              value_block_stride, value_page_stride, value_head_stride,
+                              max_blocks_per_sequence, max_sequence_length, partition_tokens,
+                              scale),
+             stream);
+}
+
+int loom_hip_paged_decode_attention_extended_f16(
+    const uint16_t* query, const void* key_cache, const void* value_cache,
+    const float* key_scales, const float* value_scales, const int32_t* block_tables,
+    const int32_t* sequence_lengths, uint16_t* output, float* lse, float* workspace,
+    uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+    uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint32_t cache_encoding, uint32_t scale_stride, uint64_t key_block_stride,
+    uint64_t key_page_stride, uint64_t key_head_stride, uint64_t value_block_stride,
+    uint64_t value_page_stride, uint64_t value_head_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, uint32_t partition_tokens, float scale, void* stream) {
+  return run(extended_problem(kF16, query, key_cache, value_cache, key_scales, value_scales,
+                              block_tables, sequence_lengths, output, lse, workspace,
+                              workspace_elements, sequences, query_heads, kv_heads, head_size,
+                              value_head_size, num_blocks, block_size, cache_encoding,
+                              scale_stride, key_block_stride, key_page_stride, key_head_stride,
+                              value_block_stride, value_page_stride, value_head_stride,
+                              max_blocks_per_sequence, max_sequence_length, partition_tokens,
+                              scale),
+             stream);
+}
+
+int loom_hip_paged_decode_attention_extended_bf16(
+    const uint16_t* query, const void* key_cache, const void* value_cache,
+    const float* key_scales, const float* value_scales, const int32_t* block_tables,
+    const int32_t* sequence_lengths, uint16_t* output, float* lse, float* workspace,
+    uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+    uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint32_t cache_encoding, uint32_t scale_stride, uint64_t key_block_stride,
+    uint64_t key_page_stride, uint64_t key_head_stride, uint64_t value_block_stride,
+    uint64_t value_page_stride, uint64_t value_head_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, uint32_t partition_tokens, float scale, void* stream) {
+  return run(extended_problem(kBf16, query, key_cache, value_cache, key_scales, value_scales,
+                              block_tables, sequence_lengths, output, lse, workspace,
+                              workspace_elements, sequences, query_heads, kv_heads, head_size,
+                              value_head_size, num_blocks, block_size, cache_encoding,
+                              scale_stride, key_block_stride, key_page_stride, key_head_stride,
+                              value_block_stride, value_page_stride, value_head_stride,
+                              max_blocks_per_sequence, max_sequence_length, partition_tokens,
+                              scale),
+             stream);
+}
+
+}  // extern "C"

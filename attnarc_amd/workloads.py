@@ -1,0 +1,269 @@
+"""Seeded synthetic paged-decode inputs for the named benchmark shapes.
+
+Every case is fully determined by its seed: sequence lengths and block tables
+come from ``numpy.random.default_rng(seed)``; Q/K/V come from a torch
+generator seeded with ``seed`` on the target device, drawn as N(0, 1) F32 and
+rounded once (round-to-nearest-even) to the storage dtype. FP8 caches are
+``fp8_e4m3fn(clamp(x / scale[kv_head], -448, 448))``, the static-scale
+encoding of docs/design/fp8-kv-cache.md:42-48 with finite saturation.
+
+Unused block-table slots hold -1 (the sentinel the reference oracle accepts
+in inactive slots, crates/loom-kernels/src/tests/attention_tests.rs:82).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+FP8_MAX = 448.0
+
+
+@dataclass
+class DecodeCase:
+    name: str
+    dtype: torch.dtype  # query / output dtype
+    cache_encoding: str  # "native" or "fp8"
+    layout: str  # "NHD" or "HND"
+    sequences: int
+    query_heads: int
+    kv_heads: int
+    head_size: int
+    value_head_size: int
+    block_size: int
+    num_blocks: int
+    max_blocks_per_sequence: int
+    lengths: list
+    partition_tokens: int
+    scale: float
+    seed: int
+    query: torch.Tensor = None
+    key_cache: torch.Tensor = None
+    value_cache: torch.Tensor = None
+    key_scales: torch.Tensor = None
+    value_scales: torch.Tensor = None
+    block_tables: torch.Tensor = None
+    sequence_lengths: torch.Tensor = None
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def max_sequence_length(self) -> int:
+        return int(max(self.lengths))
+
+    @property
+    def kv_elem_bytes(self) -> int:
+        if self.cache_encoding == "fp8":
+            return 1
+        return torch.empty((), dtype=self.dtype).element_size()
+
+    def kv_bytes(self) -> int:
+        """Algorithmic KV bytes of one call: sum(len) * Hkv * (D + Dv) * elem."""
+        return int(sum(self.lengths)) * self.kv_heads * (self.head_size + self.value_head_size) * self.kv_elem_bytes
+
+    def flops(self) -> int:
+        return 2 * int(sum(self.lengths)) * self.query_heads * (self.head_size + self.value_head_size)
+
+    def describe(self) -> dict:
+        return {
+            "workload": self.name,
+            "dtype": str(self.dtype).replace("torch.", ""),
+            "kv_cache": "fp8_e4m3fn" if self.cache_encoding == "fp8" else "native",
+            "layout": self.layout,
+            "batch": self.sequences,
+            "query_heads": self.query_heads,
+            "kv_heads": self.kv_heads,
+            "head_dim": self.head_size,
+            "block_size": self.block_size,
+            "num_blocks": self.num_blocks,
+            "context_min": int(min(self.lengths)),
+            "context_max": int(max(self.lengths)),
+            "context_sum": int(sum(self.lengths)),
+            "partition_tokens": self.partition_tokens,
+            "seed": self.seed,
+        }
+
+
+def _tables_from_pool(rng, lengths, block_size, pool_blocks, max_blocks):
+    """Assign shuffled physical blocks from a pool to each sequence in order."""
+    perm = rng.permutation(pool_blocks)
+    tables = np.full((len(lengths), max_blocks), -1, dtype=np.int32)
+    cursor = 0
+    for s, length in enumerate(lengths):
+        n = -(-int(length) // block_size)
+        tables[s, :n] = perm[cursor : cursor + n]
+        cursor += n
+    return tables
+
+
+def _randn(shape, gen, device, dtype, chunk_elems=1 << 26):
+    """N(0,1) F32 rounded to ``dtype``, generated in chunks to bound memory."""
+    out = torch.empty(shape, device=device, dtype=dtype)
+    flat = out.view(-1)
+    n = flat.numel()
+    for start in range(0, n, chunk_elems):
+        stop = min(n, start + chunk_elems)
+        flat[start:stop] = torch.randn(stop - start, generator=gen, device=device, dtype=torch.float32).to(dtype)
+    return out
+
+
+def _fp8_cache(shape, head_dim_axis, scales, gen, device, chunk_blocks=4096):
+    """fp8_e4m3fn(clamp(N(0,1) / scale[kv_head])) with the kv-head axis given."""
+    fp8 = getattr(torch, "float8_e4m3fn")
+    out = torch.empty(shape, device=device, dtype=fp8)
+    view_shape = [1, 1, 1, 1]
+    view_shape[head_dim_axis] = -1
+    inv = (1.0 / scales).view(view_shape)
+    for start in range(0, shape[0], chunk_blocks):
+        stop = min(shape[0], start + chunk_blocks)
+        x = torch.randn((stop - start,) + tuple(shape[1:]), generator=gen, device=device, dtype=torch.float32)
+        out[start:stop] = (x * inv).clamp_(-FP8_MAX, FP8_MAX).to(fp8)
+    return out
+
+
+def make_case(
+    *,
+    name: str,
+    dtype: torch.dtype,
+    sequences: int,
+    query_heads: int,
+    kv_heads: int,
+    head_size: int,
+    value_head_size: int,
+    block_size: int,
+    lengths,
+    seed: int,
+    device,
+    cache_encoding: str = "native",
+    layout: str = "NHD",
+    pool_factor: float | None = None,
+    num_blocks: int | None = None,
+    partition_tokens: int = 0,
+    scale: float | None = None,
+    scale_range=(0.01, 0.1),
+    per_head_scales: bool = True,
+) -> DecodeCase:
+    rng = np.random.default_rng(seed)
+    lengths = [int(x) for x in lengths]
+    max_len = max(lengths)
+    max_blocks = -(-max_len // block_size)
+    needed = sum(-(-l // block_size) for l in lengths)
+    if num_blocks is None:
+        num_blocks = math.ceil(needed * pool_factor) if pool_factor else sequences * max_blocks
+    num_blocks = max(num_blocks, needed)
+    tables = _tables_from_pool(rng, lengths, block_size, num_blocks, max_blocks)
+    if scale is None:
+        scale = head_size ** -0.5
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    query = _randn((sequences, query_heads, head_size), gen, device, dtype)
+    if layout == "NHD":
+        kshape = (num_blocks, block_size, kv_heads, head_size)
+        vshape = (num_blocks, block_size, kv_heads, value_head_size)
+        head_axis = 2
+    elif layout == "HND":
+        kshape = (num_blocks, kv_heads, block_size, head_size)
+        vshape = (num_blocks, kv_heads, block_size, value_head_size)
+        head_axis = 1
+    else:
+        raise ValueError(layout)
+    key_scales = value_scales = None
+    if cache_encoding == "fp8":
+        n_scales = kv_heads if per_head_scales else 1
+        lo, hi = scale_range
+        key_scales = torch.tensor(rng.uniform(lo, hi, n_scales), dtype=torch.float32, device=device)
+        value_scales = torch.tensor(rng.uniform(lo, hi, n_scales), dtype=torch.float32, device=device)
+        ks = key_scales if per_head_scales else key_scales.expand(kv_heads)
+        vs = value_scales if per_head_scales else value_scales.expand(kv_heads)
+        key_cache = _fp8_cache(kshape, head_axis, ks, gen, device)
+        value_cache = _fp8_cache(vshape, head_axis, vs, gen, device)
+    else:
+        key_cache = _randn(kshape, gen, device, dtype)
+        value_cache = _randn(vshape, gen, device, dtype)
+    return DecodeCase(
+        name=name,
+        dtype=dtype,
+        cache_encoding=cache_encoding,
+        layout=layout,
+        sequences=sequences,
+        query_heads=query_heads,
+        kv_heads=kv_heads,
+        head_size=head_size,
+        value_head_size=value_head_size,
+        block_size=block_size,
+        num_blocks=num_blocks,
+        max_blocks_per_sequence=max_blocks,
+        lengths=lengths,
+        partition_tokens=partition_tokens,
+        scale=float(scale),
+        seed=seed,
+        query=query,
+        key_cache=key_cache,
+        value_cache=value_cache,
+        key_scales=key_scales,
+        value_scales=value_scales,
+        block_tables=torch.from_numpy(tables).to(device),
+        sequence_lengths=torch.tensor(lengths, dtype=torch.int32, device=device),
+    )
+
+
+def config(index: int, device, seed: int | None = None) -> DecodeCase:
+    """The five benchmark configurations of the paged-decode north star (1-based)."""
+    seed = 1000 + index if seed is None else seed
+    rng = np.random.default_rng(seed ^ 0x5EED)
+    if index == 1:
+        # F32 MHA plumbing case: B4, H8/8, D64, len U[1,256], bs16, a seeded
+        # permutation of 64 physical blocks (16 per sequence), no split-K.
+        lengths = rng.integers(1, 257, size=4)
+        return make_case(
+            name="c1_f32_mha_plumbing", dtype=torch.float32, sequences=4, query_heads=8, kv_heads=8,
+            head_size=64, value_head_size=64, block_size=16, lengths=lengths, seed=seed, device=device,
+            num_blocks=64,
+        )
+    if index == 2:
+        # Qwen2.5-1.5B GQA: B32, H12/2, D128, len 2048, bs16, single partition.
+        return make_case(
+            name="c2_qwen2.5_1.5b_gqa_bf16", dtype=torch.bfloat16, sequences=32, query_heads=12,
+            kv_heads=2, head_size=128, value_head_size=128, block_size=16, lengths=[2048] * 32,
+            seed=seed, device=device,
+        )
+    if index == 3:
+        # Llama-3-8B GQA: B64, H32/8, D128, len U[512,8192], bs16, pool 1.25x, split-K 512.
+        lengths = rng.integers(512, 8193, size=64)
+        return make_case(
+            name="c3_llama3_8b_gqa_bf16", dtype=torch.bfloat16, sequences=64, query_heads=32,
+            kv_heads=8, head_size=128, value_head_size=128, block_size=16, lengths=lengths,
+            seed=seed, device=device, pool_factor=1.25, partition_tokens=512,
+        )
+    if index == 4:
+        # FP8-KV at Llama-3-70B head geometry: B128, H64/8, D128, len 4096, bs16, HND,
+        # per-head scales U[0.01,0.1], BF16 Q/out, split-K 512.
+        return make_case(
+            name="c4_llama3_70b_fp8kv_hnd", dtype=torch.bfloat16, sequences=128, query_heads=64,
+            kv_heads=8, head_size=128, value_head_size=128, block_size=16, lengths=[4096] * 128,
+            seed=seed, device=device, cache_encoding="fp8", layout="HND", partition_tokens=512,
+        )
+    if index == 5:
+        # Long-context MQA: B8, H32/1, D128, len U[65536,131072], bs16, split-K 1024.
+        lengths = rng.integers(65536, 131073, size=8)
+        return make_case(
+            name="c5_long_mqa_bf16", dtype=torch.bfloat16, sequences=8, query_heads=32, kv_heads=1,
+            head_size=128, value_head_size=128, block_size=16, lengths=lengths, seed=seed,
+            device=device, partition_tokens=1024,
+        )
+    raise ValueError(f"unknown config {index}")
+
+
+def run_case(case: DecodeCase, *, output=None, lse=None, workspace=None, return_lse=False):
+    """One call of the hot path for a case (extended entry point)."""
+    from .ops import paged_decode_attention_extended
+
+    return paged_decode_attention_extended(
+        case.query, case.key_cache, case.value_cache, case.block_tables, case.sequence_lengths,
+        max_sequence_length=case.max_sequence_length, scale=case.scale, layout=case.layout,
+        key_scales=case.key_scales, value_scales=case.value_scales,
+        partition_tokens=case.partition_tokens, output=output, lse=lse, workspace=workspace,
+        return_lse=return_lse,
+    )

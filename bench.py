@@ -1,0 +1,236 @@
+"""Paged-decode benchmark: µs/call and KV-read HBM GB/s on one MI355X.
+
+A step is one call of the hot path (decode kernel + split-K merge kernel)
+over one batch of the Llama-3-8B-shaped configuration (B64, Hq32/Hkv8, D128,
+BF16 NHD paged KV, ragged context U[512, 8192], block 16, pool 1.25x,
+partitions of 512 tokens), with every input already resident in HBM.
+
+value = algorithmic KV bytes per call / measured seconds per call, where the
+algorithmic bytes are sum(len) * Hkv * (D + Dv) * 2. The roofline object
+prices the decode kernel alone: the same bytes divided by that kernel's mean
+duration from HIP events recorded by the library on the launch stream.
+cpu_baseline times the CPU oracle (C++ restatement of the Rust reference
+oracle) on a bounded sample of the same workload on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c3_traffic.json")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(case, budget_s: float = 15.0):
+    """Time the oracle on a prefix sample of the sequences (kind 'port')."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    from gpu_util import to_host
+
+    oracle.lib()
+    kc = to_host(case.key_cache)
+    vc = to_host(case.value_cache)
+    q = to_host(case.query)
+    tables = to_host(case.block_tables).astype(np.int64)
+    lens = to_host(case.sequence_lengths).astype(np.int64)
+    kl = oracle.CacheLayout.nhd(case.block_size, case.kv_heads, case.head_size)
+    vl = oracle.CacheLayout.nhd(case.block_size, case.kv_heads, case.value_head_size)
+    # calibrate on one sequence, then size the sample to the budget
+    done_bytes = 0
+    elapsed = 0.0
+    used = 0
+    for s in range(case.sequences):
+        spec = oracle.spec_new(1, case.query_heads, case.kv_heads, case.head_size, case.value_head_size,
+                               case.num_blocks, case.block_size, case.max_blocks_per_sequence, int(lens[s]),
+                               case.scale, oracle.BF16)
+        t0 = time.perf_counter()
+        oracle.ext(spec, np.ascontiguousarray(q[s:s + 1]), kc, vc, np.ascontiguousarray(tables[s:s + 1]),
+                   lens[s:s + 1], key_layout=kl, value_layout=vl, want_lse=False)
+        elapsed += time.perf_counter() - t0
+        done_bytes += int(lens[s]) * case.kv_heads * (case.head_size + case.value_head_size) * 2
+        used += 1
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": done_bytes / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"first {used} of {case.sequences} sequences of the same workload "
+                  f"({sum(case.lengths[:used])} tokens, {elapsed:.1f} s, single-threaded C++ oracle, "
+                  f"F64 two-pass; host nproc={os.cpu_count()})",
+        "seconds_per_call_extrapolated": elapsed * sum(case.lengths) / max(1, sum(case.lengths[:used])),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=3, help="benchmark configuration 1-5 (metric: 3)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the decode shards by sequence/KV head with no exchange; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from attnarc_amd import ops, workloads
+    from attnarc_amd import _native
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] building config {args.config} inputs")
+    case = workloads.config(args.config, dev)
+    out = torch.empty((case.sequences, case.query_heads, case.value_head_size), device=dev, dtype=case.dtype)
+    need = ops.extended_workspace_elements(case.sequences, case.query_heads, case.value_head_size,
+                                           case.max_sequence_length, case.partition_tokens)
+    workspace = torch.empty(max(need, 1), device=dev, dtype=torch.float32) if need else None
+    kv_bytes = case.kv_bytes()
+
+    def step():
+        workloads.run_case(case, output=out, workspace=workspace)
+
+    log(f"[bench] warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    log(f"[bench] timing {args.steps} steps")
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(stop)
+    ms_per_step = ms_total / args.steps
+    value = kv_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Median of 7 samples (eager), the reference's reporting method.
+    samples = []
+    for _ in range(7):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(20):
+            step()
+        b.record()
+        torch.cuda.synchronize()
+        samples.append(a.elapsed_time(b) / 20 * 1e3)
+    samples.sort()
+    us_eager_median = samples[3]
+
+    # Per-kernel durations from events the library records on its launch stream.
+    ops.kernel_timing_enable(True)
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    dec_ms, dec_n = ops.kernel_timing_read(_native.KERNEL_DECODE)
+    mrg_ms, mrg_n = ops.kernel_timing_read(_native.KERNEL_MERGE)
+    ops.kernel_timing_enable(False)
+    dec_us = dec_ms / max(dec_n, 1) * 1e3
+    mrg_us = mrg_ms / max(mrg_n, 1) * 1e3 if mrg_n else 0.0
+    achieved = kv_bytes / (dec_us * 1e-6) / 1e9
+
+    us_graph = None
+    if not args.no_graph:
+        try:
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g):
+                for _ in range(10):
+                    step()
+            torch.cuda.synchronize()
+            gs = []
+            for _ in range(7):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(2):
+                    g.replay()
+                b.record()
+                torch.cuda.synchronize()
+                gs.append(a.elapsed_time(b) / 20 * 1e3)
+            gs.sort()
+            us_graph = gs[3]
+        except Exception as exc:  # graph capture is reported, not required
+            log(f"[bench] graph replay unavailable: {exc!r}")
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        if t.get("workload") == case.name:
+            traffic = t.get("bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(case, args.cpu_budget)
+
+    result = {
+        "metric": "paged-decode KV-read HBM GB/s (us/call alongside), 1xMI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_call": round(ms_per_step * 1e3, 2),
+        "us_per_call_eager_median7": round(us_eager_median, 2),
+        "us_per_call_graph_median7": None if us_graph is None else round(us_graph, 2),
+        "kernel_us": {"decode": round(dec_us, 2), "merge": round(mrg_us, 2)},
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if case.dtype == torch.bfloat16 else str(case.dtype).replace("torch.", ""),
+        "data": "synthetic (seeded N(0,1) Q/K/V rounded to the storage dtype, seeded lengths and shuffled block table)",
+        "config": {**case.describe(), "kv_bytes_per_call": kv_bytes, "parallelism": "none (1 GPU)"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "decode_mfma_kernel",
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

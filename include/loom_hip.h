@@ -1,0 +1,281 @@
+#ifndef LOOM_HIP_H_
+#define LOOM_HIP_H_
+
+/*
+ * loom-hip: MI355X (gfx950) launch ABI for paged MQA/GQA decode attention.
+ *
+ * Drop-in replacement for the paged-decode part of the Loom Kernels internal
+ * CUDA launch ABI (crates/loom-cuda-sys/cuda/include/loom_cuda.h). Every
+ * reference entry point keeps its argument list, argument meaning, integer
+ * widths and status codes; `void* stream` is a hipStream_t (null = the
+ * default stream). Launches are asynchronous on that stream, allocate
+ * nothing and never synchronize the host.
+ *
+ * Differences from the reference kernels, all widening the accepted set:
+ *   - no 1024-token context cap (the reference's kMaxContext,
+ *     paged_decode_attention.cu:29); the contract and CPU oracle never had
+ *     one (crates/loom-kernels/src/attention.rs:34-98);
+ *   - the split-K policy is MI355X's own (fixed-size partitions merged by a
+ *     stable log-sum-exp kernel) and is not limited to batch <= 8.
+ * Extensions (no reference counterpart in the decode ABI; vocabulary taken
+ * from the reference's RoPE+KV-write ABI, loom_cuda.h:252-318):
+ *   - FP8 E4M3FN K/V caches with static per-tensor or per-KV-head scales,
+ *   - explicit block/page/head element strides (NHD and HND views),
+ *   - an optional F32 log-sum-exp output per (sequence, query head),
+ *   - a caller-chosen split-K partition size.
+ *
+ * Metadata (block tables, sequence lengths) is trusted on the device exactly
+ * as in the reference: active sequence lengths must lie in
+ * [1, max_sequence_length] and active block IDs in [0, num_blocks).
+ */
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: loom_cuda.h:10-16. */
+enum LoomHipStatus {
+  LOOM_HIP_SUCCESS = 0,
+  LOOM_HIP_INVALID_ARGUMENT = 1,
+  LOOM_HIP_UNSUPPORTED = 2,
+  LOOM_HIP_LAUNCH_ERROR = 3,
+  LOOM_HIP_UNAVAILABLE = 4,
+};
+
+/* K/V cache encodings: loom_cuda.h:18-21 (LoomCudaKvCacheEncoding). */
+enum LoomHipKvCacheEncoding {
+  LOOM_HIP_KV_CACHE_NATIVE = 0,
+  LOOM_HIP_KV_CACHE_FP8_E4M3 = 1,
+};
+
+/* Element types of query/output: loom_cuda_bridge.h:17-21. */
+enum LoomHipDType {
+  LOOM_HIP_F32 = 0,
+  LOOM_HIP_F16 = 1,
+  LOOM_HIP_BF16 = 2,
+};
+
+/* Operator ids for launch telemetry: loom_cuda_bridge.h:28-40. */
+enum LoomHipOperator {
+  LOOM_HIP_PAGED_DECODE_ATTENTION = 9,
+};
+
+/* Kernel ids for loom_hip_kernel_timing_read. */
+enum LoomHipKernel {
+  LOOM_HIP_KERNEL_DECODE = 0, /* per-(sequence, KV head, partition) kernel */
+  LOOM_HIP_KERNEL_MERGE = 1,  /* split-K log-sum-exp merge kernel */
+};
+
+/* Replaces loom_cuda_status_string (rms_norm.cu:170-185). */
+const char* loom_hip_status_string(int status);
+
+/*
+ * Base paged decode attention. Replaces loom_cuda_paged_decode_attention_
+ * {f32,f16,bf16} (loom_cuda.h:182-212; definitions paged_decode_attention.cu:
+ * 1168-1210). Query/output are contiguous [sequences, query_heads, dim];
+ * K/V caches have dense inner NHD [block_size, kv_heads, dim] dimensions and
+ * an explicit element stride between blocks (separate caches or vLLM's
+ * interleaved [blocks, 2, block_size, kv_heads, dim] storage). F16/BF16 data
+ * is passed as uint16_t bit patterns. No workspace: each (sequence, KV head)
+ * is reduced inside one workgroup.
+ */
+int loom_hip_paged_decode_attention_f32(
+    const float* query, const float* key_cache, const float* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths,
+    float* output, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size,
+    uint32_t num_blocks, uint32_t block_size, uint64_t key_block_stride,
+    uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream);
+
+int loom_hip_paged_decode_attention_f16(
+    const uint16_t* query, const uint16_t* key_cache,
+    const uint16_t* value_cache, const int32_t* block_tables,
+    const int32_t* sequence_lengths, uint16_t* output, uint32_t sequences,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint64_t key_block_stride, uint64_t value_block_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+    float scale, void* stream);
+
+int loom_hip_paged_decode_attention_bf16(
+    const uint16_t* query, const uint16_t* key_cache,
+    const uint16_t* value_cache, const int32_t* block_tables,
+    const int32_t* sequence_lengths, uint16_t* output, uint32_t sequences,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint64_t key_block_stride, uint64_t value_block_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+    float scale, void* stream);
+
+/*
+ * Split-K workspace sizing. Replaces loom_cuda_paged_decode_attention_split_
+ * k_workspace_elements (loom_cuda.h:219-222; paged_decode_attention.cu:
+ * 1156-1166). Returns zero when the shape should use the base entry points
+ * (enough (sequence, KV head) work to fill the GPU, or a context too short to
+ * split); otherwise the F32 element count of the caller-owned workspace.
+ */
+uint64_t loom_hip_paged_decode_attention_split_k_workspace_elements(
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+    uint32_t head_size, uint32_t value_head_size,
+    uint32_t max_sequence_length);
+
+/*
+ * Split-K paged decode attention. Replaces loom_cuda_paged_decode_attention_
+ * split_k_{f32,f16,bf16} (loom_cuda.h:224-250; paged_decode_attention.cu:
+ * 1212-1276). `workspace` must hold at least the element count returned by
+ * the sizing function for the same shape, which must be non-zero.
+ */
+int loom_hip_paged_decode_attention_split_k_f32(
+    const float* query, const float* key_cache, const float* value_cache,
+    const int32_t* block_tables, const int32_t* sequence_lengths,
+    float* output, float* workspace, uint64_t workspace_elements,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+    uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint64_t key_block_stride,
+    uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream);
+
+int loom_hip_paged_decode_attention_split_k_f16(
+    const uint16_t* query, const uint16_t* key_cache,
+    const uint16_t* value_cache, const int32_t* block_tables,
+    const int32_t* sequence_lengths, uint16_t* output, float* workspace,
+    uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size,
+    uint32_t num_blocks, uint32_t block_size, uint64_t key_block_stride,
+    uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream);
+
+int loom_hip_paged_decode_attention_split_k_bf16(
+    const uint16_t* query, const uint16_t* key_cache,
+    const uint16_t* value_cache, const int32_t* block_tables,
+    const int32_t* sequence_lengths, uint16_t* output, float* workspace,
+    uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size,
+    uint32_t num_blocks, uint32_t block_size, uint64_t key_block_stride,
+    uint64_t value_block_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, float scale, void* stream);
+
+/*
+ * Extended entry points (no reference counterpart in the decode ABI; they
+ * replace nothing and add FP8 KV, strides, LSE and fixed partitions).
+ *
+ * Workspace for the extended entry points: returns B*Hq*P*(Dv+2) F32
+ * elements with P = ceil(max_sequence_length / partition_tokens), or zero
+ * when P <= 1 or partition_tokens == 0 (single partition, no workspace).
+ */
+uint64_t loom_hip_paged_decode_attention_extended_workspace_elements(
+    uint32_t sequences, uint32_t query_heads, uint32_t value_head_size,
+    uint32_t max_sequence_length, uint32_t partition_tokens);
+
+/*
+ * Query/output are contiguous [sequences, query_heads, dim] of the entry
+ * point's dtype. The caches are logical [num_blocks, block_size, kv_heads,
+ * dim] views with unit dim stride and the given block/page/head element
+ * strides: NHD is (bs*Hkv*D, Hkv*D, D), HND is (Hkv*bs*D, D, bs*D).
+ * cache_encoding NATIVE: cache elements have the query dtype and the scale
+ * pointers must be null. FP8_E4M3: cache elements are OCP E4M3FN bytes and
+ * the logical value is fp8_to_f32(byte) * scale[kv_head * scale_stride]
+ * (scale_stride 0 = per tensor, 1 = per KV head; scales finite, > 0).
+ * `lse` (nullable) receives [sequences, query_heads] F32 natural-log
+ * log-sum-exp of the scaled scores. partition_tokens == 0 means one
+ * partition per sequence. The workspace must be null with zero elements when
+ * the sizing function returns 0, and hold at least that many otherwise.
+ */
+int loom_hip_paged_decode_attention_extended_f32(
+    const float* query, const void* key_cache, const void* value_cache,
+    const float* key_scales, const float* value_scales,
+    const int32_t* block_tables, const int32_t* sequence_lengths,
+    float* output, float* lse, float* workspace, uint64_t workspace_elements,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+    uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint32_t cache_encoding, uint32_t scale_stride,
+    uint64_t key_block_stride, uint64_t key_page_stride,
+    uint64_t key_head_stride, uint64_t value_block_stride,
+    uint64_t value_page_stride, uint64_t value_head_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+    uint32_t partition_tokens, float scale, void* stream);
+
+int loom_hip_paged_decode_attention_extended_f16(
+    const uint16_t* query, const void* key_cache, const void* value_cache,
+    const float* key_scales, const float* value_scales,
+    const int32_t* block_tables, const int32_t* sequence_lengths,
+    uint16_t* output, float* lse, float* workspace,
+    uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size,
+    uint32_t num_blocks, uint32_t block_size, uint32_t cache_encoding,
+    uint32_t scale_stride, uint64_t key_block_stride,
+    uint64_t key_page_stride, uint64_t key_head_stride,
+    uint64_t value_block_stride, uint64_t value_page_stride,
+    uint64_t value_head_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, uint32_t partition_tokens, float scale,
+    void* stream);
+
+int loom_hip_paged_decode_attention_extended_bf16(
+    const uint16_t* query, const void* key_cache, const void* value_cache,
+    const float* key_scales, const float* value_scales,
+    const int32_t* block_tables, const int32_t* sequence_lengths,
+    uint16_t* output, float* lse, float* workspace,
+    uint64_t workspace_elements, uint32_t sequences, uint32_t query_heads,
+    uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size,
+    uint32_t num_blocks, uint32_t block_size, uint32_t cache_encoding,
+    uint32_t scale_stride, uint64_t key_block_stride,
+    uint64_t key_page_stride, uint64_t key_head_stride,
+    uint64_t value_block_stride, uint64_t value_page_stride,
+    uint64_t value_head_stride, uint32_t max_blocks_per_sequence,
+    uint32_t max_sequence_length, uint32_t partition_tokens, float scale,
+    void* stream);
+
+/*
+ * Capability query. Replaces the PagedDecodeAttention arms of
+ * CudaBackend::supports (crates/loom-cuda/src/cuda_backend.rs:112-134,
+ * attention_dispatch.rs:330-344). Reports without launching work. Returns
+ * LOOM_HIP_SUCCESS when the shape is executable, LOOM_HIP_UNSUPPORTED or
+ * LOOM_HIP_INVALID_ARGUMENT otherwise, with a static reason in *reason
+ * (nullable). *kernel_family (nullable) receives "mfma" for the matrix-core
+ * kernel or "vector" for the general kernel.
+ */
+int loom_hip_paged_decode_attention_supports(
+    uint32_t dtype, uint32_t cache_encoding, uint32_t sequences,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+    float scale, const char** reason, const char** kernel_family);
+
+/* Backend name, as CudaBackend::name() = "loom-cuda" (cuda_backend.rs:43). */
+const char* loom_hip_backend_name(void);
+
+/* ABI version (loom-cuda-bridge reports 2, cuda/mod.rs:720-724). */
+uint32_t loom_hip_abi_version(void);
+
+/*
+ * Thread-local message describing the last failed call on this thread
+ * (replaces loom_cuda_bridge_last_error_message, cuda/mod.rs:726-731).
+ */
+const char* loom_hip_last_error_message(void);
+
+/*
+ * Relaxed atomic launch counters (replace loom_cuda_bridge_launch_count /
+ * _reset_launch_count, cuda/mod.rs:733-774). One successful decode call
+ * counts once regardless of how many kernels it launches.
+ */
+int loom_hip_launch_count(uint32_t operation, uint64_t* count);
+int loom_hip_reset_launch_count(uint32_t operation);
+
+/*
+ * Per-kernel timing for profiling (no reference counterpart). When enabled,
+ * every launch is bracketed by events on the launch stream; reading
+ * synchronizes the recorded events and returns the accumulated milliseconds
+ * and launch count since the last reset. Enabling resets the totals.
+ */
+int loom_hip_kernel_timing_enable(uint32_t enable);
+int loom_hip_kernel_timing_read(uint32_t kernel, double* total_ms,
+                                uint64_t* launches);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* LOOM_HIP_H_ */
