@@ -13,7 +13,8 @@ import threading
 
 from . import build as _build
 
-LIB_PATH = _build.LIB_PATH
+# LOOM_HIP_LIBRARY selects another build of the same ABI (e.g. for A/B runs).
+LIB_PATH = os.environ.get("LOOM_HIP_LIBRARY", _build.LIB_PATH)
 
 SUCCESS = 0
 INVALID_ARGUMENT = 1

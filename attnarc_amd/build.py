@@ -14,6 +14,8 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 SOURCE = os.path.join(PKG_DIR, "csrc", "paged_decode_attention.hip")
 LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip.so")
+PROBE_SOURCE = os.path.join(PKG_DIR, "csrc", "hbm_probe.hip")
+PROBE_LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 OFFLOAD_ARCH = "gfx950"
 
@@ -28,15 +30,20 @@ HIPCC_FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile the library; returns its path. Raises on compiler failure."""
-    os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *HIPCC_FLAGS, SOURCE, "-o", tmp]
+def _compile(source: str, out: str, verbose: bool) -> None:
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [HIPCC, *HIPCC_FLAGS, source, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the decode library and the HBM probe library; returns the former's path."""
+    _compile(SOURCE, LIB_PATH, verbose)
+    _compile(PROBE_SOURCE, PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 

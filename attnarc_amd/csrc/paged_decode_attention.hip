@@ -136,10 +136,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_fence_lds() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  return 0.0f;
-}
+// Orders this wave's LDS accesses in the compiler only. The LDS unit
+// executes one wave's DS instructions in issue order, so a write followed by
+// a read of the same bytes (by any lanes of the wave) needs no hardware wait;
+// a memory fence here would also wait for every outstanding global load.
+__device__ __forceinline__ void wave_fence_lds() { asm volatile("" ::: "memory"); }
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maxima).
+__device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // ---------------------------------------------------------------------------
 // General kernel: any head size, dtype, stride and group size.
@@ -297,11 +301,18 @@ constexpr uint32_t kTileBytes = kChunk * kTileRowBytes;  // 8 KiB V tile per wav
 template <typename QE>
 struct MfmaOps;
 
+typedef short s16x4m __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
 template <>
 struct MfmaOps<Bf16Elem> {
   using vec8 = bf16x8;
+  using vec4 = s16x4m;
   static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
   // Eight FP8 E4M3FN bytes (two dwords) to eight 16-bit values, exactly.
   static __device__ __forceinline__ vec8 from_fp8(uint32_t lo, uint32_t hi) {
@@ -320,8 +331,12 @@ struct MfmaOps<Bf16Elem> {
 template <>
 struct MfmaOps<F16Elem> {
   using vec8 = f16x8;
+  using vec4 = f16x4;
   static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ vec8 from_fp8(uint32_t lo, uint32_t hi) {
     const f16x2 a0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
@@ -336,23 +351,82 @@ struct MfmaOps<F16Elem> {
   }
 };
 
-// Loads of one 32-token chunk held in registers.
-//   16-bit caches: k[sb][kc] = 8 dims of token sb*16 + (lane & 15) at dims
-//   kc*32 + (lane >> 4)*8; v[i] = 8 dims (lane & 15)*8 of token
-//   4*i + (lane >> 4).
-//   FP8 caches: k[sb][j] = 16 bytes of token sb*16 + (lane & 15) at dims
-//   j*64 + (lane >> 4)*16; v[i] = 16 bytes (lane & 7)*16 of token
-//   8*i + (lane >> 3).
-template <bool kFp8>
-struct ChunkRegs {
-  static constexpr int kKLoads = kFp8 ? 2 : 4;
-  static constexpr int kVLoads = kFp8 ? 4 : 8;
-  u32x4 k[2][kKLoads];
-  u32x4 v[kVLoads];
-};
-
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *static_cast<const u32x4*>(p);
+}
+
+// ---------------------------------------------------------------------------
+// Hand-scheduled memory pipeline. The decode loop's global loads are issued
+// as inline assembly, which the compiler's wait-count insertion does not see,
+// and every consumer is preceded by an explicit s_waitcnt vmcnt(N) that also
+// names the destination registers as in/out operands (so no use of them can
+// be scheduled above it). Vector-memory loads of a wave complete in issue
+// order, so vmcnt(N) guarantees every load except the N most recent ones.
+// (The compiler's own insertion waits for all outstanding loads at this
+// loop's header and before DS instructions while LDS DMA is in flight, which
+// would drain the prefetch pipeline on every chunk.)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void vm_load16(u32x4& dst, const void* p) {
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(p));
+}
+
+__device__ __forceinline__ void vm_load4(int32_t& dst, const void* p) {
+  asm volatile("global_load_dword %0, %1, off" : "=v"(dst) : "v"(p));
+}
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (M0 holds the wave-uniform LDS base).
+__device__ __forceinline__ void vm_load16_lds(const void* p, uint8_t* lds) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(p), "s"(base) : "memory", "m0");
+}
+
+// Registers of one in-flight 32-token chunk plus the block IDs of the chunk
+// two steps later.
+//   16-bit caches: k[sb*4 + kc] = 8 dims kc*32 + (lane >> 4)*8 of token
+//   sb*16 + (lane & 15), already in the QK^T MFMA operand layout; V goes
+//   global -> LDS by DMA and has no registers.
+//   FP8 caches: k[sb*2 + j] = 16 bytes at dims j*64 + (lane >> 4)*16 of the
+//   same token; v[i] = 16 bytes (lane & 7)*16 of token 8*i + (lane >> 3).
+template <bool kFp8>
+struct ChunkBuf {
+  static constexpr int kK = kFp8 ? 4 : 8;
+  static constexpr int kLoads = kFp8 ? 8 : 16;  // vector-memory loads per chunk
+  u32x4 k[kK];
+  u32x4 v[4];
+  int32_t ids;
+};
+
+// s_waitcnt vmcnt(N) bound to one chunk buffer's registers.
+template <int N>
+__device__ __forceinline__ void vm_wait(ChunkBuf<false>& b) {
+  asm volatile("s_waitcnt vmcnt(%9)"
+               : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.k[2]), "+v"(b.k[3]), "+v"(b.k[4]), "+v"(b.k[5]),
+                 "+v"(b.k[6]), "+v"(b.k[7]), "+v"(b.ids)
+               : "n"(N)
+               : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait(ChunkBuf<true>& b) {
+  asm volatile("s_waitcnt vmcnt(%9)"
+               : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.k[2]), "+v"(b.k[3]), "+v"(b.v[0]), "+v"(b.v[1]),
+                 "+v"(b.v[2]), "+v"(b.v[3]), "+v"(b.ids)
+               : "n"(N)
+               : "memory");
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// V tile in LDS: 32 token rows of 128 16-bit values (8 KiB). The 16-byte
+// chunk ch of row t sits at chunk ch ^ 2*(t & 3): the transposed reads below
+// (per 16-lane group: four rows t = 4g + k, 32 consecutive bytes each) then
+// touch four disjoint 32-byte bank groups.
+__device__ __forceinline__ uint32_t tile_off(uint32_t t, uint32_t ch) {
+  return t * kTileRowBytes + ((ch ^ ((t & 3U) << 1)) << 4);
 }
 
 template <typename QE, bool kFp8, int kHeadTiles>
@@ -360,14 +434,13 @@ struct MfmaDecoder {
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using CT = typename std::conditional<kFp8, uint8_t, uint16_t>::type;
-  static constexpr uint32_t kElem = kFp8 ? 1 : 2;
+  using Buf = ChunkBuf<kFp8>;
 
   const DecodeArgs& a;
-  uint32_t lane, g, c, seq, kvh, p0, p1;
+  uint32_t lane, g, c, p1;
   const int32_t* table;
   const CT* kbase;  // key cache + kv_head offset
   const CT* vbase;
-  uint8_t* tile;  // this wave's LDS V tile
   float sl2;
 
   vec8 qb[kHeadTiles][4];
@@ -377,122 +450,126 @@ struct MfmaDecoder {
 
   __device__ __forceinline__ MfmaDecoder(const DecodeArgs& args) : a(args) {}
 
-  // Logical-block IDs for the chunk starting at c0: lane i holds the table
-  // entry of logical block (c0 >> shift) + i, for the blocks the chunk's
-  // clamped tokens touch.
-  __device__ __forceinline__ int32_t fetch_ids(uint32_t c0) const {
+  // Lane i loads the table entry of logical block (c0 >> shift) + i (at most
+  // 32 blocks per chunk); lanes past the chunk's last block reload the last
+  // entry, so the load is branch-free.
+  __device__ __forceinline__ void fetch_ids(int32_t& ids, uint32_t c0) const {
     const uint32_t lb0 = c0 >> a.block_shift;
     const uint32_t last = (min(c0 + kChunk, p1) - 1U) >> a.block_shift;
-    int32_t id = 0;
-    if (lb0 + lane <= last) id = table[lb0 + lane];
-    return id;
+    vm_load4(ids, table + min(lb0 + lane, last));
   }
 
   // Element offset of the row of token t (clamped into the partition).
-  __device__ __forceinline__ void row_of(uint32_t c0, int32_t ids, uint32_t t, uint64_t stride_b,
-                                         uint64_t stride_p, uint64_t* off) const {
+  __device__ __forceinline__ uint64_t row_of(uint32_t c0, int32_t ids, uint32_t t, uint64_t stride_b,
+                                             uint64_t stride_p) const {
     t = min(t, p1 - 1U);
     const uint32_t src = (t >> a.block_shift) - (c0 >> a.block_shift);
     const uint32_t blk = static_cast<uint32_t>(__shfl(ids, static_cast<int>(src), 64));
     const uint32_t page = t & (a.block_size - 1U);
-    *off = static_cast<uint64_t>(blk) * stride_b + static_cast<uint64_t>(page) * stride_p;
+    return static_cast<uint64_t>(blk) * stride_b + static_cast<uint64_t>(page) * stride_p;
   }
 
-  __device__ __forceinline__ void issue(ChunkRegs<kFp8>& r, int32_t ids, uint32_t c0) const {
+  __device__ __forceinline__ void issue_k(Buf& b, int32_t ids, uint32_t c0) const {
+    constexpr int kPerRow = kFp8 ? 2 : 4;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      uint64_t off;
-      row_of(c0, ids, c0 + sb * 16 + c, a.k_block, a.k_page, &off);
-      const CT* p = kbase + off;
+      const CT* p = kbase + row_of(c0, ids, c0 + sb * 16 + c, a.k_block, a.k_page);
 #pragma unroll
-      for (int j = 0; j < ChunkRegs<kFp8>::kKLoads; ++j) {
+      for (int j = 0; j < kPerRow; ++j) {
         const uint32_t dim = kFp8 ? (j * 64 + g * 16) : (j * 32 + g * 8);
-        r.k[sb][j] = load16(p + dim);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < ChunkRegs<kFp8>::kVLoads; ++i) {
-      const uint32_t t = kFp8 ? (c0 + 8 * i + (lane >> 3)) : (c0 + 4 * i + (lane >> 4));
-      uint64_t off;
-      row_of(c0, ids, t, a.v_block, a.v_page, &off);
-      const uint32_t dim = kFp8 ? (lane & 7U) * 16 : (lane & 15U) * 8;
-      r.v[i] = load16(vbase + off + dim);
-    }
-  }
-
-  // LDS V tile: 32 rows of 128 16-bit values; the 16-byte chunk ch of row t
-  // is stored at chunk ch ^ (2 * ((t >> 2) & 3)) so that the transposed
-  // reads below (four token rows 4 apart, 16 consecutive dims) hit 32
-  // distinct banks.
-  static __device__ __forceinline__ uint32_t tile_off(uint32_t t, uint32_t ch) {
-    return t * kTileRowBytes + ((ch ^ (((t >> 2) & 3U) << 1)) << 4);
-  }
-
-  __device__ __forceinline__ void stage_v(const ChunkRegs<kFp8>& r) const {
-#pragma unroll
-    for (int i = 0; i < ChunkRegs<kFp8>::kVLoads; ++i) {
-      if (kFp8) {
-        const uint32_t t = 8 * i + (lane >> 3);
-        const uint32_t ch = (lane & 7U) * 2;
-        const vec8 lo = Ops::from_fp8(r.v[i][0], r.v[i][1]);
-        const vec8 hi = Ops::from_fp8(r.v[i][2], r.v[i][3]);
-        *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = lo;
-        *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = hi;
-      } else {
-        const uint32_t t = 4 * i + (lane >> 4);
-        const uint32_t ch = lane & 15U;
-        *reinterpret_cast<u32x4*>(tile + tile_off(t, ch)) = r.v[i];
+        vm_load16(b.k[sb * kPerRow + j], p + dim);
       }
     }
   }
 
-  __device__ __forceinline__ vec8 k_operand(const ChunkRegs<kFp8>& r, int sb, int kc) const {
+  // 16-bit V: eight global -> LDS DMA loads of 1 KiB. Load i fills tile rows
+  // 4i..4i+3 in lane order (lane l -> byte 16*l), so lane l fetches the
+  // logical chunk that the swizzle places at its slot.
+  __device__ __forceinline__ void issue_v_dma(uint8_t* tile, int32_t ids, uint32_t c0) const {
+    const uint32_t ch = (lane & 15U) ^ (((lane >> 4) & 3U) << 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t t = c0 + 4 * i + (lane >> 4);
+      vm_load16_lds(vbase + row_of(c0, ids, t, a.v_block, a.v_page) + ch * 8, tile + i * 1024);
+    }
+  }
+
+  __device__ __forceinline__ void issue_v_fp8(Buf& b, int32_t ids, uint32_t c0) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = c0 + 8 * i + (lane >> 3);
+      vm_load16(b.v[i], vbase + row_of(c0, ids, t, a.v_block, a.v_page) + (lane & 7U) * 16);
+    }
+  }
+
+  // One chunk's loads, in the order the steady state uses: V, K (FP8) or
+  // K, V (16-bit); the IDs of chunk n + 2 follow separately.
+  __device__ __forceinline__ void issue_chunk(Buf& b, uint8_t* tile, int32_t ids, uint32_t c0) const {
     if (kFp8) {
-      const u32x4 w = r.k[sb][kc >> 1];
+      issue_v_fp8(b, ids, c0);
+      issue_k(b, ids, c0);
+    } else {
+      issue_k(b, ids, c0);
+      issue_v_dma(tile, ids, c0);
+    }
+  }
+
+  // FP8 V: exact conversion to 16-bit values, written in the tile layout.
+  __device__ __forceinline__ void stage_v_fp8(const Buf& b, uint8_t* tile) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = 8 * i + (lane >> 3);
+      const uint32_t ch = (lane & 7U) * 2;
+      const vec8 lo = Ops::from_fp8(b.v[i][0], b.v[i][1]);
+      const vec8 hi = Ops::from_fp8(b.v[i][2], b.v[i][3]);
+      *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = lo;
+      *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = hi;
+    }
+  }
+
+  __device__ __forceinline__ vec8 k_operand(const Buf& b, int sb, int kc) const {
+    if (kFp8) {
+      const u32x4 w = b.k[sb * 2 + (kc >> 1)];
       return (kc & 1) ? Ops::from_fp8(w[2], w[3]) : Ops::from_fp8(w[0], w[1]);
     } else {
-      return __builtin_bit_cast(vec8, r.k[sb][kc]);
+      return __builtin_bit_cast(vec8, b.k[sb * 4 + kc]);
     }
   }
 
-  // PV A operand: V^T[dims dt*16 + c][8 token slots of lane group g]; slot j
-  // of group g is token (j >> 2) * 16 + 4g + (j & 3), the token whose
-  // probability the QK output placed in this lane.
-  __device__ __forceinline__ vec8 v_operand(uint32_t dt) const {
-    const uint32_t d = dt * 16 + c;
-    const uint32_t ch = d >> 3;
-    const uint32_t e = (d & 7U) * 2;
-    uint16_t x[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t t = (j >> 2) * 16 + 4 * g + (j & 3);
-      x[j] = *reinterpret_cast<const uint16_t*>(tile + tile_off(t, ch) + e);
-    }
-    u32x4 w;
-    w[0] = x[0] | (static_cast<uint32_t>(x[1]) << 16);
-    w[1] = x[2] | (static_cast<uint32_t>(x[3]) << 16);
-    w[2] = x[4] | (static_cast<uint32_t>(x[5]) << 16);
-    w[3] = x[6] | (static_cast<uint32_t>(x[7]) << 16);
+  // PV A operand: V^T[dims dt*16 + c][8 token slots of lane group g] by two
+  // transposed reads. In a 16-lane group, ds_read_b64_tr_b16 hands lane i,
+  // element k, the 16-bit element i % 4 of the 8 bytes addressed by lane
+  // 4k + i / 4; lane (k = c >> 2, q = c & 3) therefore addresses dims
+  // dt*16 + 4q of token 4g + k, and lane c receives dim dt*16 + c of tokens
+  // 4g + k (first read) and 16 + 4g + k (second read): token slot j of group g
+  // is token (j >> 2) * 16 + 4g + (j & 3), where the QK output placed P.
+  __device__ __forceinline__ vec8 v_operand(const uint8_t* tile, uint32_t dt) const {
+    const uint32_t k = c >> 2, q = c & 3U;
+    const uint32_t off = tile_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
+    lds_u8* base = (lds_u8*)tile;  // generic -> LDS address space
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off + 16 * kTileRowBytes));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(vec8, w);
   }
 
-  // Second half of a chunk: QK^T, online softmax and PV. The chunk's V has
-  // already been staged into the LDS tile.
-  __device__ __forceinline__ void compute(const ChunkRegs<kFp8>& r, uint32_t c0) {
-
-    // S[token 4g + r][head c] for the two 16-token halves of the chunk.
-    f32x4 s[kHeadTiles][2];
+  // QK^T of one chunk: S[token 4g + r][head c] for its two 16-token halves.
+  __device__ __forceinline__ void qk(const Buf& b, f32x4 (&s)[kHeadTiles][2]) const {
 #pragma unroll
     for (int ht = 0; ht < kHeadTiles; ++ht) {
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) z = Ops::mma(k_operand(r, sb, kc), qb[ht][kc], z);
+        for (int kc = 0; kc < 4; ++kc) z = Ops::mma(k_operand(b, sb, kc), qb[ht][kc], z);
         s[ht][sb] = z;
       }
     }
+  }
 
+  // Online softmax and PV of one chunk whose V is in `tile`.
+  __device__ __forceinline__ void softmax_pv(f32x4 (&s)[kHeadTiles][2], uint32_t c0, const uint8_t* tile) {
     vec8 pb[kHeadTiles];
 #pragma unroll
     for (int ht = 0; ht < kHeadTiles; ++ht) {
@@ -529,29 +606,61 @@ struct MfmaDecoder {
       w[3] = Ops::pack2(p[6], p[7]);
       pb[ht] = __builtin_bit_cast(vec8, w);
     }
-
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; ++dt) {
-      const vec8 va = v_operand(dt);
+      const vec8 va = v_operand(tile, dt);
 #pragma unroll
       for (int ht = 0; ht < kHeadTiles; ++ht) acc[ht][dt] = Ops::mma(va, pb[ht], acc[ht][dt]);
     }
+  }
+
+  // Pipeline step for chunk n held in buffer b / tile. Every step issues the
+  // same loads: chunk n + 2 into b and the tile (K once QK^T has consumed
+  // b.k, V once PV has read the tile or, for FP8, once it is staged) and the
+  // block IDs of chunk n + 4. Chunks past the wave's last one are not
+  // skipped: their tokens clamp to the partition's last row, so those loads
+  // hit in cache and are never consumed. With a uniform issue pattern the
+  // loads in flight on entry are always, oldest first, chunk n's group and
+  // chunk n + 1's group (L loads + 1 ID load each), so one wait of
+  // vmcnt(L + 1) completes exactly chunk n's group.
+  __device__ __forceinline__ void step(Buf& b, uint8_t* tile, uint32_t cn, uint32_t stride_tokens) {
+    vm_wait<Buf::kLoads + 1>(b);
+    const uint32_t c2 = cn + 2 * stride_tokens;
+    if (kFp8) {
+      stage_v_fp8(b, tile);
+      wave_fence_lds();
+      issue_v_fp8(b, b.ids, c2);
+    }
+    f32x4 s[kHeadTiles][2];
+    qk(b, s);
+    issue_k(b, b.ids, c2);
+    softmax_pv(s, cn, tile);
+    if (!kFp8) {
+      wait_lds_reads();  // the tile's transposed reads have returned before the DMA refills it
+      issue_v_dma(tile, b.ids, c2);
+    }
     wave_fence_lds();
+    fetch_ids(b.ids, cn + 4 * stride_tokens);
   }
 };
 
-template <typename QE, bool kFp8, int kHeadTiles>
-__global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kernel(DecodeArgs a) {
+template <typename QE, bool kFp8, int kHeadTiles, int kWaves>
+__global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) {
   using Dec = MfmaDecoder<QE, kFp8, kHeadTiles>;
   using vec8 = typename Dec::vec8;
   using CT = typename Dec::CT;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  using Buf = typename Dec::Buf;
+  __shared__ __attribute__((aligned(16))) uint8_t tile0[kWaves * kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t tile1[kWaves * kTileBytes];
 
+  // KV head fastest: the workgroups of one (sequence, partition) are
+  // dispatched together (one per XCD for 8 KV heads), so the per-head slices
+  // of each paged block are read at about the same time.
   const uint32_t bid = blockIdx.x;
-  const uint32_t part = bid % a.parts;
-  const uint32_t rest = bid / a.parts;
-  const uint32_t kvh = rest % a.kv_heads;
-  const uint32_t seq = rest / a.kv_heads;
+  const uint32_t kvh = bid % a.kv_heads;
+  const uint32_t rest = bid / a.kv_heads;
+  const uint32_t part = rest % a.parts;
+  const uint32_t seq = rest / a.parts;
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
   const uint32_t p0 = part * a.partition_tokens;
   if (p0 >= len) return;  // uniform across the workgroup
@@ -560,18 +669,13 @@ __global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kerne
   dec.lane = threadIdx.x & 63U;
   dec.g = dec.lane >> 4;
   dec.c = dec.lane & 15U;
-  dec.seq = seq;
-  dec.kvh = kvh;
-  dec.p0 = p0;
   dec.p1 = min(p0 + a.partition_tokens, len);
   dec.table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
   dec.kbase = static_cast<const CT*>(a.key_cache) + static_cast<uint64_t>(kvh) * a.k_head;
   dec.vbase = static_cast<const CT*>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head;
-  const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t waves = blockDim.x >> 6;
-  const uint32_t state_bytes = kHeadTiles * 16 * (kDim + 2) * 4;
-  const uint32_t wave_bytes = state_bytes > kTileBytes ? state_bytes : kTileBytes;
-  dec.tile = smem + wave * wave_bytes;
+  const uint32_t wave = kWaves == 1 ? 0U : (threadIdx.x >> 6);
+  uint8_t* tA = tile0 + wave * kTileBytes;
+  uint8_t* tB = tile1 + wave * kTileBytes;
 
   float k_scale = 1.0f, v_scale = 1.0f;
   if (kFp8) {
@@ -580,17 +684,43 @@ __global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kerne
   }
   dec.sl2 = a.score_scale_log2 * k_scale;
 
-  // Query operand: head ht*16 + c, the dims paired with this lane's K dims.
+  // Chunks of this partition: chunk k covers [p0 + 32k, p0 + 32k + 32); wave
+  // w takes chunks w, w + waves, ...
+  const uint32_t nck = (dec.p1 - p0 + kChunk - 1) / kChunk;
+  const uint32_t my_n = nck > wave ? (nck - wave + kWaves - 1) / kWaves : 0;
+  const uint32_t st = kWaves * kChunk;
+  const uint32_t c0 = p0 + wave * kChunk;
+
+  // Query operand (head ht*16 + c, the dims paired with this lane's K dims)
+  // and the first two chunks' block IDs; then everything is waited for.
   const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
                          (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group) * kDim;
+  u32x4 qw[kHeadTiles][4];
 #pragma unroll
   for (int ht = 0; ht < kHeadTiles; ++ht) {
-    const uint32_t h = ht * 16 + dec.c;
+    const uint32_t h = min(ht * 16 + dec.c, a.group - 1U);  // rows >= group are zeroed below
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
-      u32x4 w = {0U, 0U, 0U, 0U};
-      if (h < a.group) w = load16(qrow + h * kDim + dim);
+      vm_load16(qw[ht][kc], qrow + h * kDim + dim);
+    }
+  }
+  Buf bA, bB;
+  int32_t ids0, ids1;
+  dec.fetch_ids(ids0, c0);
+  dec.fetch_ids(ids1, c0 + st);
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(ids0), "+v"(ids1) : : "memory");
+#pragma unroll
+  for (int ht = 0; ht < kHeadTiles; ++ht) {
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) asm volatile("s_waitcnt vmcnt(0)" : "+v"(qw[ht][kc]));
+  }
+#pragma unroll
+  for (int ht = 0; ht < kHeadTiles; ++ht) {
+    const bool live = ht * 16 + dec.c < a.group;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const u32x4 w = live ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U};
       dec.qb[ht][kc] = __builtin_bit_cast(vec8, w);
     }
     dec.m[ht] = -INFINITY;
@@ -599,37 +729,22 @@ __global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kerne
     for (int dt = 0; dt < 8; ++dt) dec.acc[ht][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // Chunks of this partition: chunk k covers [p0 + 32k, p0 + 32k + 32); wave
-  // w takes chunks w, w + waves, ...
-  const uint32_t nck = (dec.p1 - p0 + kChunk - 1) / kChunk;
-  const uint32_t my_n = nck > wave ? (nck - wave + waves - 1) / waves : 0;
-  const uint32_t stride_tokens = waves * kChunk;
-  uint32_t cA = p0 + wave * kChunk;
   if (my_n > 0) {
-    // Two register buffers in ping-pong. Per step: fetch block IDs two
-    // chunks ahead, stage the current chunk's V into LDS (freeing its
-    // registers), issue the next chunk's K/V loads, then compute the current
-    // chunk while those loads are in flight.
-    ChunkRegs<kFp8> bufA, bufB;
-    int32_t idsA = dec.fetch_ids(cA);
-    int32_t idsB = my_n > 1 ? dec.fetch_ids(cA + stride_tokens) : 0;
-    dec.issue(bufA, idsA, cA);
-    for (uint32_t i = 0; i < my_n; i += 2) {
-      const uint32_t cB = cA + stride_tokens;
-      if (i + 2 < my_n) idsA = dec.fetch_ids(cB + stride_tokens);
-      dec.stage_v(bufA);
-      wave_fence_lds();
-      if (i + 1 < my_n) dec.issue(bufB, idsB, cB);
-      dec.compute(bufA, cA);
-      if (i + 1 >= my_n) break;
-      const uint32_t cC = cB + stride_tokens;
-      if (i + 3 < my_n) idsB = dec.fetch_ids(cC + stride_tokens);
-      dec.stage_v(bufB);
-      wave_fence_lds();
-      if (i + 2 < my_n) dec.issue(bufA, idsA, cC);
-      dec.compute(bufB, cB);
-      cA = cC;
+    // Prologue in steady-state order: chunk 0, IDs of chunk 2, chunk 1, IDs
+    // of chunk 3 (missing chunks clamp, as in step()).
+    dec.issue_chunk(bA, tA, ids0, c0);
+    dec.fetch_ids(bA.ids, c0 + 2 * st);
+    dec.issue_chunk(bB, tB, ids1, c0 + st);
+    dec.fetch_ids(bB.ids, c0 + 3 * st);
+    for (uint32_t n = 0; n < my_n; n += 2) {
+      const uint32_t cn = c0 + n * st;
+      dec.step(bA, tA, cn, st);
+      if (n + 1 >= my_n) break;
+      dec.step(bB, tB, cn + st, st);
     }
+    // Drain the trailing (clamped) loads: DMA into the tiles must land
+    // before the tiles are reused below.
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   }
 
   // Per-lane partial denominators -> per head (sum over the 4 lane groups).
@@ -641,43 +756,483 @@ __global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kerne
     dec.lsum[ht] = l;
   }
 
-  // Workgroup reduction: each wave publishes (m, l, O[h][d]) in its LDS slot.
-  float* st = reinterpret_cast<float*>(dec.tile);
-  __syncthreads();  // every wave is done with its V tile
+  const uint32_t heads = min(a.group, static_cast<uint32_t>(kHeadTiles * 16));
+  if (kWaves == 1) {
+    // One wave: write straight from the accumulators. Lane (g, c) holds
+    // dims dt*16 + 4g + r of head c.
+#pragma unroll
+    for (int ht = 0; ht < kHeadTiles; ++ht) {
+      const uint32_t h = ht * 16 + dec.c;
+      if (h >= heads) continue;
+      const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h;
+      const float M = dec.m[ht], L = dec.lsum[ht];
+      if (a.parts == 1) {
+        const float inv = v_scale / L;
+        uint16_t* o = static_cast<uint16_t*>(a.output) + row * kDim + 4 * dec.g;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          uint32_t w0 = QE::from_f(dec.acc[ht][dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[ht][dt][1] * inv)) << 16);
+          uint32_t w1 = QE::from_f(dec.acc[ht][dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[ht][dt][3] * inv)) << 16);
+          *reinterpret_cast<uint2*>(o + dt * 16) = make_uint2(w0, w1);
+        }
+        if (a.lse != nullptr && dec.g == 0) a.lse[row] = (M + log2f(L)) * kLn2;
+      } else {
+        const uint64_t state = row * a.parts + part;
+        float* o = a.ws_o + state * kDim + 4 * dec.g;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          *reinterpret_cast<float4*>(o + dt * 16) =
+              make_float4(dec.acc[ht][dt][0] * v_scale, dec.acc[ht][dt][1] * v_scale,
+                          dec.acc[ht][dt][2] * v_scale, dec.acc[ht][dt][3] * v_scale);
+        }
+        if (dec.g == 0) {
+          a.ws_ml[state * 2] = M;
+          a.ws_ml[state * 2 + 1] = L;
+        }
+      }
+    }
+    return;
+  }
+
+  // Several waves: reduce through LDS one head tile at a time. Wave w
+  // publishes O[16 heads][128 dims] in its tile0 slot and (m, l) per head in
+  // its tile1 slot.
+  float* so = reinterpret_cast<float*>(tA);
+  float* sml = reinterpret_cast<float*>(tB);
 #pragma unroll
   for (int ht = 0; ht < kHeadTiles; ++ht) {
-    const uint32_t h = ht * 16 + dec.c;
-    float* hs = st + h * (kDim + 2);
+    __syncthreads();  // tiles are free (loop done / previous tile consumed)
     if (dec.g == 0) {
-      hs[0] = dec.m[ht];
-      hs[1] = dec.lsum[ht];
+      sml[dec.c * 2] = dec.m[ht];
+      sml[dec.c * 2 + 1] = dec.lsum[ht];
     }
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
+      *reinterpret_cast<f32x4*>(so + dec.c * kDim + dt * 16 + 4 * dec.g) = dec.acc[ht][dt];
+    }
+    __syncthreads();
+    const uint32_t tile_heads = heads > ht * 16U ? min(16U, heads - ht * 16U) : 0U;
+    for (uint32_t idx = threadIdx.x; idx < tile_heads * kDim; idx += kWaves * 64) {
+      const uint32_t hl = idx / kDim;
+      const uint32_t d = idx % kDim;
+      float M = -INFINITY;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) hs[2 + dt * 16 + 4 * dec.g + rr] = dec.acc[ht][dt][rr];
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, reinterpret_cast<const float*>(tile1 + w * kTileBytes)[hl * 2]);
+      float L = 0.0f, O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float* wml = reinterpret_cast<const float*>(tile1 + w * kTileBytes);
+        const float* wo = reinterpret_cast<const float*>(tile0 + w * kTileBytes);
+        const float f = exp2f(wml[hl * 2] - M);  // 0 for a wave that had no chunk
+        L = fmaf(wml[hl * 2 + 1], f, L);
+        O = fmaf(wo[hl * kDim + d], f, O);
+      }
+      O *= v_scale;
+      const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + ht * 16 + hl;
+      if (a.parts == 1) {
+        static_cast<uint16_t*>(a.output)[row * kDim + d] = QE::from_f(O / L);
+        if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
+      } else {
+        const uint64_t state = row * a.parts + part;
+        a.ws_o[state * kDim + d] = O;
+        if (d == 0) {
+          a.ws_ml[state * 2] = M;
+          a.ws_ml[state * 2 + 1] = L;
+        }
+      }
     }
   }
-  __syncthreads();
+}
 
-  const uint32_t heads = min(a.group, static_cast<uint32_t>(kHeadTiles * 16));
-  for (uint32_t idx = threadIdx.x; idx < heads * kDim; idx += blockDim.x) {
-    const uint32_t h = idx / kDim;
-    const uint32_t d = idx % kDim;
-    float M = -INFINITY;
-    for (uint32_t w = 0; w < waves; ++w) {
-      const float* hs = reinterpret_cast<const float*>(smem + w * wave_bytes) + h * (kDim + 2);
-      M = fmaxf(M, hs[0]);
+// ---------------------------------------------------------------------------
+// Streaming matrix-core kernel: 16-token steps, four waves per SIMD.
+//
+// Measured on MI355X, a random paged read reaches ~5.8 TB/s only with ~32
+// waves per CU; with 8 waves per CU it stays near 3.2 TB/s however many bytes
+// each wave keeps in flight. This kernel is therefore sized for 16 waves per
+// CU: each wave keeps two 16-token steps in flight with K in registers
+// (2 x 16 VGPRs) and V DMA'd into two 4 KiB LDS tiles, and stays within 128
+// VGPRs. It applies when the block size is a power of two >= 16 and steps are
+// aligned to 16 tokens, so each step lies in one block: the block ID is a
+// scalar load, the row base is scalar arithmetic, and every load uses a
+// loop-invariant per-lane 32-bit offset from that scalar base.
+//
+// Per step: QK^T with v_mfma_f32_16x16x32 (S[token 4g + r][head c] lands in
+// lane (g, c)); PV with v_mfma_f32_16x16x16, whose B operand is exactly that
+// S layout (4 tokens of lane group g) and whose A operand (dims dt*16 + c of
+// tokens 4g + k) is one ds_read_b64_tr_b16.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kStep = 16;
+constexpr uint32_t kStepTileBytes = kStep * kTileRowBytes;  // 4 KiB
+
+template <bool kFp8>
+struct StepBuf {
+  static constexpr int kK = kFp8 ? 2 : 4;      // 16-byte K loads per lane
+  static constexpr int kLoads = kFp8 ? 4 : 8;  // vector-memory instructions per step
+  u32x4 k[kK];
+  u32x4 v[2];  // FP8 V (16-bit V goes to LDS by DMA)
+};
+
+template <int N>
+__device__ __forceinline__ void vm_wait(StepBuf<false>& b) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.k[2]), "+v"(b.k[3]) : "n"(N) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait(StepBuf<true>& b) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.v[0]), "+v"(b.v[1]) : "n"(N) : "memory");
+}
+
+// Loads with a wave-uniform 64-bit base and a per-lane 32-bit byte offset.
+template <int kImm>
+__device__ __forceinline__ void vm_load16_sv(u32x4& dst, uint32_t voff, uint64_t base) {
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(dst) : "v"(voff), "s"(base), "n"(kImm));
+}
+
+__device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds)));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+}
+
+template <typename QE, bool kFp8>
+struct StreamDecoder {
+  using Ops = MfmaOps<QE>;
+  using vec8 = typename Ops::vec8;
+  using vec4 = typename Ops::vec4;
+  using Buf = StepBuf<kFp8>;
+  static constexpr uint32_t kElem = kFp8 ? 1 : 2;
+
+  const DecodeArgs& a;
+  uint32_t lane, g, c;
+  uint32_t p1;   // end of this partition (exclusive)
+  uint32_t len;  // sequence length
+  uint32_t last_block;  // last active logical block of the sequence
+  const int32_t* table;
+  uint64_t kbase, vbase;  // byte address of (block 0, page 0, this kv head)
+  uint64_t kstride_b, vstride_b, kstride_p, vstride_p;  // byte strides
+  uint32_t k_voff;   // lane's K offset: page c, dims (lane >> 4)*8 (16-bit) or *16 (FP8)
+  uint32_t v_voff;   // 16-bit: lane's DMA offset within a 4-row group; FP8: page lane >> 2, bytes (lane & 3)*32
+  float sl2;
+
+  vec8 qb[4];
+  f32x4 acc[8];  // O^T: dims dt*16 + 4g + r, head c
+  float m;       // running max (log2 units) of head c
+  float lsum;    // partial denominator over this lane's tokens
+
+  __device__ __forceinline__ StreamDecoder(const DecodeArgs& args) : a(args) {}
+
+  // Physical block of the step starting at token t0 (clamped to the last
+  // active block, so steps past the sequence stay in valid memory).
+  __device__ __forceinline__ uint32_t block_of(uint32_t t0) const {
+    const uint32_t lb = min(t0 >> a.block_shift, last_block);
+    return static_cast<uint32_t>(table[lb]);
+  }
+
+  __device__ __forceinline__ uint64_t row_base(uint64_t base, uint64_t stride_b, uint64_t stride_p, uint32_t blk,
+                                               uint32_t t0) const {
+    return base + blk * stride_b + (t0 & (a.block_size - 1U)) * stride_p;
+  }
+
+  __device__ __forceinline__ void issue(Buf& b, uint8_t* tile, uint32_t blk, uint32_t t0) const {
+    const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
+    const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
+    if (kFp8) {
+      vm_load16_sv<0>(b.v[0], v_voff, vb);
+      vm_load16_sv<16>(b.v[1], v_voff, vb);
+      vm_load16_sv<0>(b.k[0], k_voff, kb);
+      vm_load16_sv<64>(b.k[1], k_voff, kb);
+    } else {
+      vm_load16_sv<0>(b.k[0], k_voff, kb);
+      vm_load16_sv<64>(b.k[1], k_voff, kb);
+      vm_load16_sv<128>(b.k[2], k_voff, kb);
+      vm_load16_sv<192>(b.k[3], k_voff, kb);
     }
+  }
+
+  // 16-bit V: four 1 KiB DMA loads, rows 4i..4i+3 of the tile each.
+  __device__ __forceinline__ void issue_v_dma(uint8_t* tile, uint32_t blk, uint32_t t0) const {
+    const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vm_load16_lds_sv(v_voff, vb + 4 * i * vstride_p, tile + i * 1024);
+  }
+
+  // FP8 V: 32 bytes of token lane >> 2 -> 32 16-bit values (rows past the
+  // sequence end become zero), four 16-byte chunks of the tile row.
+  __device__ __forceinline__ void stage_v_fp8(const Buf& b, uint8_t* tile, uint32_t t0) const {
+    const uint32_t t = lane >> 2;
+    const bool live = t0 + t < len;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 w = live ? b.v[h] : u32x4{0U, 0U, 0U, 0U};
+      const uint32_t ch = (lane & 3U) * 4 + h * 2;
+      *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = Ops::from_fp8(w[0], w[1]);
+      *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = Ops::from_fp8(w[2], w[3]);
+    }
+  }
+
+  // Tile rows of tokens past the sequence end (possible only in its last
+  // step) may hold unwritten cache slots: zero them so P = 0 meets a finite V.
+  __device__ __forceinline__ void zero_dead_rows(uint8_t* tile, uint32_t t0) const {
+    if (t0 + kStep <= len) return;  // uniform
+    const uint32_t t = lane >> 2;   // 4 lanes per row, 64 bytes each
+    if (t0 + t >= len) {
+      u32x4* row = reinterpret_cast<u32x4*>(tile + t * kTileRowBytes + (lane & 3U) * 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
+    }
+  }
+
+  __device__ __forceinline__ vec8 k_operand(const Buf& b, int kc) const {
+    if (kFp8) {
+      const u32x4 w = b.k[kc >> 1];
+      return (kc & 1) ? Ops::from_fp8(w[2], w[3]) : Ops::from_fp8(w[0], w[1]);
+    } else {
+      return __builtin_bit_cast(vec8, b.k[kc]);
+    }
+  }
+
+  __device__ __forceinline__ f32x4 qk(const Buf& b) const {
+    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) z = Ops::mma(k_operand(b, kc), qb[kc], z);
+    return z;
+  }
+
+  __device__ __forceinline__ void softmax_pv(f32x4 s, uint32_t t0, const uint8_t* tile) {
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = t0 + 4 * g + r < p1 ? s[r] * sl2 : -INFINITY;
+      s[r] = v;
+      cmax = fmaxf(cmax, v);
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    const float mn = fmaxf(m, cmax);  // finite: every step has a valid token
+    // Rescale only when some head's maximum moved (exact; usually skipped).
+    if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      m = mn;
+    }
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(s[r] - m);
+      lsum += p[r];
+    }
+    const uint32_t w0 = Ops::pack2(p[0], p[1]), w1 = Ops::pack2(p[2], p[3]);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const vec4 pb = __builtin_bit_cast(vec4, u32x2{w0, w1});
+    const uint32_t k = c >> 2, q = c & 3U;
+    lds_u8* base = (lds_u8*)tile;
+#pragma unroll
+    for (uint32_t dt = 0; dt < 8; ++dt) {
+      const uint32_t off = tile_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
+      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
+      acc[dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb, acc[dt]);
+    }
+  }
+};
+
+template <typename QE, bool kFp8, int kSplit>
+__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(4)))
+void decode_stream_kernel(DecodeArgs a) {
+  using Dec = StreamDecoder<QE, kFp8>;
+  using Buf = typename Dec::Buf;
+  using vec8 = typename Dec::vec8;
+  __shared__ __attribute__((aligned(16))) uint8_t tile0[kSplit * kStepTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t tile1[kSplit * kStepTileBytes];
+
+  // KV head fastest (see decode_mfma_kernel).
+  const uint32_t bid = blockIdx.x;
+  const uint32_t kvh = bid % a.kv_heads;
+  const uint32_t rest = bid / a.kv_heads;
+  const uint32_t part = rest % a.parts;
+  const uint32_t seq = rest / a.parts;
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const uint32_t p0 = part * a.partition_tokens;
+  if (p0 >= len) return;
+
+  Dec dec(a);
+  dec.lane = threadIdx.x & 63U;
+  dec.g = dec.lane >> 4;
+  dec.c = dec.lane & 15U;
+  dec.len = len;
+  dec.p1 = min(p0 + a.partition_tokens, len);
+  dec.last_block = (len - 1U) >> a.block_shift;
+  dec.table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
+  constexpr uint32_t es = Dec::kElem;
+  dec.kstride_b = a.k_block * es;
+  dec.vstride_b = a.v_block * es;
+  dec.kstride_p = a.k_page * es;
+  dec.vstride_p = a.v_page * es;
+  dec.kbase = reinterpret_cast<uint64_t>(a.key_cache) + static_cast<uint64_t>(kvh) * a.k_head * es;
+  dec.vbase = reinterpret_cast<uint64_t>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head * es;
+  dec.k_voff = static_cast<uint32_t>(dec.c * dec.kstride_p) + (kFp8 ? dec.g * 16 : dec.g * 16);
+  if (kFp8) {
+    dec.v_voff = static_cast<uint32_t>((dec.lane >> 2) * dec.vstride_p) + (dec.lane & 3U) * 32;
+  } else {
+    // DMA slot of lane l in a 4-row group: row l >> 4, physical chunk l & 15,
+    // which holds logical chunk (l & 15) ^ 2*(row & 3).
+    const uint32_t ch = (dec.lane & 15U) ^ (((dec.lane >> 4) & 3U) << 1);
+    dec.v_voff = static_cast<uint32_t>((dec.lane >> 4) * dec.vstride_p) + ch * 16;
+  }
+  const uint32_t wave = kSplit == 1 ? 0U : (threadIdx.x >> 6);
+  uint8_t* tA = tile0 + wave * kStepTileBytes;
+  uint8_t* tB = tile1 + wave * kStepTileBytes;
+
+  float k_scale = 1.0f, v_scale = 1.0f;
+  if (kFp8) {
+    k_scale = a.key_scales[kvh * a.scale_stride];
+    v_scale = a.value_scales[kvh * a.scale_stride];
+  }
+  dec.sl2 = a.score_scale_log2 * k_scale;
+
+  // Steps of this partition: step k covers [p0 + 16k, p0 + 16k + 16); wave
+  // w takes steps w, w + kSplit, ...; steps past the wave's last one are
+  // clamped onto it (re-reads that hit in cache), keeping the issue uniform.
+  const uint32_t nst = (dec.p1 - p0 + kStep - 1) / kStep;
+  const uint32_t my_n = nst > wave ? (nst - wave + kSplit - 1) / kSplit : 0;
+  const uint32_t st = kSplit * kStep;
+  const uint32_t t_first = p0 + wave * kStep;
+  const uint32_t t_last = t_first + (my_n > 0 ? my_n - 1 : 0) * st;
+
+  const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
+                         (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group) * kDim;
+  {
+    const uint32_t h = min(dec.c, a.group - 1U);
+    u32x4 qw[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
+      vm_load16(qw[kc], qrow + h * kDim + dim);
+    }
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) asm volatile("s_waitcnt vmcnt(0)" : "+v"(qw[kc]));
+    const bool live = dec.c < a.group;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
+  }
+  dec.m = -INFINITY;
+  dec.lsum = 0.0f;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) dec.acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (my_n > 0) {
+    constexpr int L = Buf::kLoads;
+    Buf bA, bB;
+    // Block IDs run two steps ahead of the loads that use them.
+    uint32_t blk0 = dec.block_of(t_first);
+    uint32_t blk1 = dec.block_of(min(t_first + st, t_last));
+    uint32_t nextA = dec.block_of(min(t_first + 2 * st, t_last));
+    uint32_t nextB = dec.block_of(min(t_first + 3 * st, t_last));
+    dec.issue(bA, tA, blk0, t_first);
+    if (!kFp8) dec.issue_v_dma(tA, blk0, t_first);
+    dec.issue(bB, tB, blk1, min(t_first + st, t_last));
+    if (!kFp8) dec.issue_v_dma(tB, blk1, min(t_first + st, t_last));
+    for (uint32_t n = 0; n < my_n; ++n) {
+      Buf& b = (n & 1) ? bB : bA;
+      uint8_t* tile = (n & 1) ? tB : tA;
+      uint32_t& next = (n & 1) ? nextB : nextA;
+      const uint32_t t0 = t_first + n * st;
+      const uint32_t t2 = min(t0 + 2 * st, t_last);
+      vm_wait<L>(b);  // this step's loads; the next step's L stay in flight
+      if (kFp8) {
+        dec.stage_v_fp8(b, tile, t0);
+        wave_fence_lds();
+        const uint64_t vb = dec.row_base(dec.vbase, dec.vstride_b, dec.vstride_p, next, t2);
+        vm_load16_sv<0>(b.v[0], dec.v_voff, vb);
+        vm_load16_sv<16>(b.v[1], dec.v_voff, vb);
+      } else {
+        dec.zero_dead_rows(tile, t0);
+        wave_fence_lds();
+      }
+      const f32x4 s = dec.qk(b);
+      {
+        const uint64_t kb = dec.row_base(dec.kbase, dec.kstride_b, dec.kstride_p, next, t2);
+        vm_load16_sv<0>(b.k[0], dec.k_voff, kb);
+        vm_load16_sv<64>(b.k[1], dec.k_voff, kb);
+        if (!kFp8) {
+          vm_load16_sv<128>(b.k[2], dec.k_voff, kb);
+          vm_load16_sv<192>(b.k[3], dec.k_voff, kb);
+        }
+      }
+      dec.softmax_pv(s, t0, tile);
+      if (!kFp8) {
+        wait_lds_reads();
+        dec.issue_v_dma(tile, next, t2);
+      }
+      wave_fence_lds();
+      next = dec.block_of(min(t0 + 4 * st, t_last));
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  }
+
+  float l = dec.lsum;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const uint32_t h = dec.c;
+  const bool head_live = h < a.group;
+  if (kSplit == 1) {
+    if (!head_live) return;
+    const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h;
+    if (a.parts == 1) {
+      const float inv = v_scale / l;
+      uint16_t* o = static_cast<uint16_t*>(a.output) + row * kDim + 4 * dec.g;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        uint32_t w0 = QE::from_f(dec.acc[dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][1] * inv)) << 16);
+        uint32_t w1 = QE::from_f(dec.acc[dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(o + dt * 16) = make_uint2(w0, w1);
+      }
+      if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m + log2f(l)) * kLn2;
+    } else {
+      const uint64_t state = row * a.parts + part;
+      float* o = a.ws_o + state * kDim + 4 * dec.g;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        *reinterpret_cast<float4*>(o + dt * 16) = make_float4(dec.acc[dt][0] * v_scale, dec.acc[dt][1] * v_scale,
+                                                             dec.acc[dt][2] * v_scale, dec.acc[dt][3] * v_scale);
+      }
+      if (dec.g == 0) {
+        a.ws_ml[state * 2] = dec.m;
+        a.ws_ml[state * 2 + 1] = l;
+      }
+    }
+    return;
+  }
+
+  // Several waves split the partition: reduce through LDS. Each wave's O
+  // [16 heads][128 dims] needs 8 KiB: tile0 and tile1 slots of that wave are
+  // adjacent only per array, so O goes to tile0 (rows 0..7 of 16 heads... )
+  __shared__ float red_o[kSplit][16][kDim];
+  __shared__ float red_ml[kSplit][16][2];
+  if (dec.g == 0) {
+    red_ml[wave][h][0] = dec.m;
+    red_ml[wave][h][1] = l;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&red_o[wave][h][dt * 16 + 4 * dec.g]) = dec.acc[dt];
+  __syncthreads();
+  const uint32_t heads = min(a.group, 16U);
+  for (uint32_t idx = threadIdx.x; idx < heads * kDim; idx += kSplit * 64) {
+    const uint32_t hl = idx / kDim, d = idx % kDim;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSplit; ++w) M = fmaxf(M, red_ml[w][hl][0]);
     float L = 0.0f, O = 0.0f;
-    for (uint32_t w = 0; w < waves; ++w) {
-      const float* hs = reinterpret_cast<const float*>(smem + w * wave_bytes) + h * (kDim + 2);
-      const float f = exp2f(hs[0] - M);  // 0 for a wave that had no chunk
-      L = fmaf(hs[1], f, L);
-      O = fmaf(hs[2 + d], f, O);
+#pragma unroll
+    for (int w = 0; w < kSplit; ++w) {
+      const float f = exp2f(red_ml[w][hl][0] - M);
+      L = fmaf(red_ml[w][hl][1], f, L);
+      O = fmaf(red_o[w][hl][d], f, O);
     }
     O *= v_scale;
-    const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h;
+    const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + hl;
     if (a.parts == 1) {
       static_cast<uint16_t*>(a.output)[row * kDim + d] = QE::from_f(O / L);
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
@@ -693,17 +1248,23 @@ __global__ __launch_bounds__(kHeadTiles == 1 ? 512 : 256) void decode_mfma_kerne
 }
 
 // ---------------------------------------------------------------------------
-// Split-K merge: one workgroup per (sequence, query head) row. Only the
-// ceil(len / partition_tokens) partitions that hold tokens are read.
+// Split-K merge: one workgroup of 256 threads per (sequence, query head) row.
+// Only the ceil(len / partition_tokens) partitions that hold tokens are read.
+// Factors f_p = 2^(m_p - M) go to LDS; then wave w accumulates partitions
+// p = w mod 4 for 2 dims per lane (unrolled for loads in flight), and the
+// four partial sums are added in LDS.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kMergeThreads = 128;
-constexpr uint32_t kMergeWindow = 512;
+constexpr uint32_t kMergeThreads = 256;
+constexpr uint32_t kMergeWaves = kMergeThreads / 64;
+constexpr uint32_t kMergeWindow = 2048;
+constexpr uint32_t kMergeDimsPerPass = 128;
 
 template <typename QE>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
   using QT = typename QE::T;
   __shared__ float factor[kMergeWindow];
-  __shared__ float red[kMergeThreads / 64];
+  __shared__ float red[kMergeWaves];
+  __shared__ float part[kMergeWaves][kMergeDimsPerPass];
   const uint32_t row = blockIdx.x;
   const uint32_t seq = row / a.query_heads;
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
@@ -721,7 +1282,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
   if (lane == 0) red[wave] = M;
   __syncthreads();
   M = red[0];
-  for (uint32_t w = 1; w < kMergeThreads / 64; ++w) M = fmaxf(M, red[w]);
+#pragma unroll
+  for (uint32_t w = 1; w < kMergeWaves; ++w) M = fmaxf(M, red[w]);
   __syncthreads();
 
   float Lp = 0.0f;
@@ -731,25 +1293,56 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
   if (lane == 0) red[wave] = Lp;
   __syncthreads();
   float L = 0.0f;
-  for (uint32_t w = 0; w < kMergeThreads / 64; ++w) L += red[w];
+#pragma unroll
+  for (uint32_t w = 0; w < kMergeWaves; ++w) L += red[w];
   const float inv = 1.0f / L;
 
   const uint32_t Dv = a.value_head_size;
-  for (uint32_t d0 = 0; d0 < Dv; d0 += kMergeThreads) {
-    const uint32_t d = d0 + tid;
-    float O = 0.0f;
+  for (uint32_t d0 = 0; d0 < Dv; d0 += kMergeDimsPerPass) {
+    const uint32_t d_a = d0 + lane, d_b = d0 + 64 + lane;
+    float acc_a = 0.0f, acc_b = 0.0f;
     for (uint32_t w0 = 0; w0 < n; w0 += kMergeWindow) {
       const uint32_t wn = min(kMergeWindow, n - w0);
       __syncthreads();
       for (uint32_t p = tid; p < wn; p += kMergeThreads) factor[p] = exp2f(ml[2 * (w0 + p)] - M);
       __syncthreads();
-      if (d < Dv) {
-        for (uint32_t p = 0; p < wn; ++p) {
-          O = fmaf(os[static_cast<uint64_t>(w0 + p) * Dv + d], factor[p], O);
-        }
+      uint32_t p = wave;
+      for (; p + 3 * kMergeWaves < wn; p += 4 * kMergeWaves) {
+        const float* o0 = os + static_cast<uint64_t>(w0 + p) * Dv;
+        const float* o1 = o0 + kMergeWaves * static_cast<uint64_t>(Dv);
+        const float* o2 = o1 + kMergeWaves * static_cast<uint64_t>(Dv);
+        const float* o3 = o2 + kMergeWaves * static_cast<uint64_t>(Dv);
+        const float a0 = d_a < Dv ? o0[d_a] : 0.0f, b0 = d_b < Dv ? o0[d_b] : 0.0f;
+        const float a1 = d_a < Dv ? o1[d_a] : 0.0f, b1 = d_b < Dv ? o1[d_b] : 0.0f;
+        const float a2 = d_a < Dv ? o2[d_a] : 0.0f, b2 = d_b < Dv ? o2[d_b] : 0.0f;
+        const float a3 = d_a < Dv ? o3[d_a] : 0.0f, b3 = d_b < Dv ? o3[d_b] : 0.0f;
+        const float f0 = factor[p], f1 = factor[p + kMergeWaves];
+        const float f2 = factor[p + 2 * kMergeWaves], f3 = factor[p + 3 * kMergeWaves];
+        acc_a = fmaf(a0, f0, acc_a);
+        acc_b = fmaf(b0, f0, acc_b);
+        acc_a = fmaf(a1, f1, acc_a);
+        acc_b = fmaf(b1, f1, acc_b);
+        acc_a = fmaf(a2, f2, acc_a);
+        acc_b = fmaf(b2, f2, acc_b);
+        acc_a = fmaf(a3, f3, acc_a);
+        acc_b = fmaf(b3, f3, acc_b);
+      }
+      for (; p < wn; p += kMergeWaves) {
+        const float* o0 = os + static_cast<uint64_t>(w0 + p) * Dv;
+        if (d_a < Dv) acc_a = fmaf(o0[d_a], factor[p], acc_a);
+        if (d_b < Dv) acc_b = fmaf(o0[d_b], factor[p], acc_b);
       }
     }
-    if (d < Dv) static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * Dv + d] = QE::from_f(O * inv);
+    part[wave][lane] = acc_a;
+    part[wave][64 + lane] = acc_b;
+    __syncthreads();
+    if (tid < kMergeDimsPerPass && d0 + tid < Dv) {
+      float O = 0.0f;
+#pragma unroll
+      for (uint32_t w = 0; w < kMergeWaves; ++w) O += part[w][tid];
+      static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * Dv + d0 + tid] = QE::from_f(O * inv);
+    }
+    __syncthreads();
   }
   if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
 }
@@ -991,15 +1584,20 @@ int launch_merge(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
-template <typename QE, bool kFp8, int kHT>
-int launch_mfma(const DecodeArgs& args, uint64_t grid, uint32_t waves, hipStream_t stream) {
-  const uint32_t state_bytes = kHT * 16 * (kDim + 2) * 4;
-  const uint32_t wave_bytes = state_bytes > kTileBytes ? state_bytes : kTileBytes;
-  const size_t shared = static_cast<size_t>(waves) * wave_bytes;
+template <typename QE, bool kFp8, int kHT, int kWaves>
+int launch_mfma(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  hipLaunchKernelGGL((decode_mfma_kernel<QE, kFp8, kHT>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(waves * 64), shared, stream, args);
+  hipLaunchKernelGGL((decode_mfma_kernel<QE, kFp8, kHT, kWaves>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(kWaves * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
+template <typename QE, bool kFp8, int kHT>
+int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hipStream_t stream) {
+  // One wave per workgroup up to 32 chunks per partition, four beyond (a
+  // long single partition would otherwise leave most CUs idle).
+  return chunks <= 32 ? launch_mfma<QE, kFp8, kHT, 1>(args, grid, stream)
+                      : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
 template <typename QE, typename CE>
@@ -1060,16 +1658,12 @@ int run_typed(const Problem& p, hipStream_t stream) {
       return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
     args.grid_y = p.kv_heads;
     const uint32_t chunks = (partition_tokens + kChunk - 1) / kChunk;
-    const int ht = group > 16 ? 2 : 1;
-    const uint32_t max_waves = ht == 1 ? 8 : 4;
-    uint32_t waves = (chunks + 3) / 4;
-    waves = waves < 1 ? 1 : (waves > max_waves ? max_waves : waves);
-    if (ht == 1) {
-      status = fp8 ? launch_mfma<QE, true, 1>(args, grid, waves, stream)
-                   : launch_mfma<QE, false, 1>(args, grid, waves, stream);
+    if (group > 16) {
+      status = fp8 ? launch_mfma_waves<QE, true, 2>(args, grid, chunks, stream)
+                   : launch_mfma_waves<QE, false, 2>(args, grid, chunks, stream);
     } else {
-      status = fp8 ? launch_mfma<QE, true, 2>(args, grid, waves, stream)
-                   : launch_mfma<QE, false, 2>(args, grid, waves, stream);
+      status = fp8 ? launch_mfma_waves<QE, true, 1>(args, grid, chunks, stream)
+                   : launch_mfma_waves<QE, false, 1>(args, grid, chunks, stream);
     }
     }
   } else {

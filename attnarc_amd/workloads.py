@@ -209,8 +209,17 @@ def make_case(
     )
 
 
-def config(index: int, device, seed: int | None = None) -> DecodeCase:
-    """The five benchmark configurations of the paged-decode north star (1-based)."""
+def config(index: int, device, seed: int | None = None, layout: str | None = None) -> DecodeCase:
+    """The five benchmark configurations of the paged-decode north star (1-based).
+
+    ``layout`` overrides the configuration's cache layout (NHD/HND) for
+    layout comparisons; the default is the configuration's own.
+    """
+    case = _config(index, device, seed, layout)
+    return case
+
+
+def _config(index: int, device, seed, layout) -> DecodeCase:
     seed = 1000 + index if seed is None else seed
     rng = np.random.default_rng(seed ^ 0x5EED)
     if index == 1:
@@ -220,14 +229,14 @@ def config(index: int, device, seed: int | None = None) -> DecodeCase:
         return make_case(
             name="c1_f32_mha_plumbing", dtype=torch.float32, sequences=4, query_heads=8, kv_heads=8,
             head_size=64, value_head_size=64, block_size=16, lengths=lengths, seed=seed, device=device,
-            num_blocks=64,
+            num_blocks=64, layout=layout or "NHD",
         )
     if index == 2:
         # Qwen2.5-1.5B GQA: B32, H12/2, D128, len 2048, bs16, single partition.
         return make_case(
             name="c2_qwen2.5_1.5b_gqa_bf16", dtype=torch.bfloat16, sequences=32, query_heads=12,
             kv_heads=2, head_size=128, value_head_size=128, block_size=16, lengths=[2048] * 32,
-            seed=seed, device=device,
+            seed=seed, device=device, layout=layout or "NHD",
         )
     if index == 3:
         # Llama-3-8B GQA: B64, H32/8, D128, len U[512,8192], bs16, pool 1.25x, split-K 512.
@@ -235,7 +244,7 @@ def config(index: int, device, seed: int | None = None) -> DecodeCase:
         return make_case(
             name="c3_llama3_8b_gqa_bf16", dtype=torch.bfloat16, sequences=64, query_heads=32,
             kv_heads=8, head_size=128, value_head_size=128, block_size=16, lengths=lengths,
-            seed=seed, device=device, pool_factor=1.25, partition_tokens=512,
+            seed=seed, device=device, pool_factor=1.25, partition_tokens=512, layout=layout or "NHD",
         )
     if index == 4:
         # FP8-KV at Llama-3-70B head geometry: B128, H64/8, D128, len 4096, bs16, HND,
@@ -243,7 +252,7 @@ def config(index: int, device, seed: int | None = None) -> DecodeCase:
         return make_case(
             name="c4_llama3_70b_fp8kv_hnd", dtype=torch.bfloat16, sequences=128, query_heads=64,
             kv_heads=8, head_size=128, value_head_size=128, block_size=16, lengths=[4096] * 128,
-            seed=seed, device=device, cache_encoding="fp8", layout="HND", partition_tokens=512,
+            seed=seed, device=device, cache_encoding="fp8", layout=layout or "HND", partition_tokens=512,
         )
     if index == 5:
         # Long-context MQA: B8, H32/1, D128, len U[65536,131072], bs16, split-K 1024.
@@ -251,7 +260,7 @@ def config(index: int, device, seed: int | None = None) -> DecodeCase:
         return make_case(
             name="c5_long_mqa_bf16", dtype=torch.bfloat16, sequences=8, query_heads=32, kv_heads=1,
             head_size=128, value_head_size=128, block_size=16, lengths=lengths, seed=seed,
-            device=device, partition_tokens=1024,
+            device=device, partition_tokens=1024, layout=layout or "NHD",
         )
     raise ValueError(f"unknown config {index}")
 

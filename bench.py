@@ -32,6 +32,94 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def hbm_probe(kind: str, nbytes: int = 4 << 30, iters: int = 10, per_cu=(4, 8, 16, 32)):
+    """Attainable HBM bandwidth on this box: the best of a streaming read (or
+    copy) of ``nbytes`` over grids of ``per_cu`` 256-thread workgroups per CU."""
+    import ctypes
+
+    import torch
+
+    from attnarc_amd import build as _b
+
+    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
+    lib.loom_hip_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint32,
+                                               ctypes.c_void_p]
+    lib.loom_hip_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32,
+                                        ctypes.c_void_p]
+    props = torch.cuda.get_device_properties(0)
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
+    sink = torch.empty(props.multi_processor_count * max(per_cu) * 256, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src) if kind == "copy" else None
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    best = 0.0
+    for k in per_cu:
+        best = max(best, _probe_once(lib, kind, src, dst, sink, nbytes, props.multi_processor_count * k, stream, iters))
+    return best
+
+
+def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
+    import torch
+
+    def once():
+        if kind == "copy":
+            rc = lib.loom_hip_probe_copy(src.data_ptr(), dst.data_ptr(), nbytes, blocks, stream)
+        else:
+            rc = lib.loom_hip_probe_stream_read(src.data_ptr(), nbytes, sink.data_ptr(), blocks, stream)
+        assert rc == 0, rc
+
+    once()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        once()
+    b.record()
+    torch.cuda.synchronize()
+    sec = a.elapsed_time(b) / iters * 1e-3
+    moved = nbytes * (2 if kind == "copy" else 1)
+    return moved / sec / 1e9
+
+
+def gather_probe(chunk_bytes: int, total_bytes: int = 2 << 30, iters: int = 10, per_cu: int = 16,
+                 unroll: int = 8) -> float:
+    """Bandwidth of reading ``total_bytes`` as randomly permuted chunks of
+    ``chunk_bytes`` (the granularity of a paged K/V access pattern)."""
+    import ctypes
+
+    import torch
+
+    from attnarc_amd import build as _b
+
+    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
+    lib.loom_hip_probe_gather_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                               ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    chunks = total_bytes // chunk_bytes
+    base = torch.empty(total_bytes // 4, dtype=torch.int32, device="cuda").fill_(3)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    perm = torch.randperm(chunks, generator=g, device="cuda").to(torch.int32)
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count * per_cu
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def once():
+        rc = lib.loom_hip_probe_gather_read(base.data_ptr(), perm.data_ptr(), chunks, chunk_bytes,
+                                            sink.data_ptr(), blocks, unroll, stream)
+        assert rc == 0, rc
+
+    once()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        once()
+    b.record()
+    torch.cuda.synchronize()
+    return total_bytes / (a.elapsed_time(b) / iters * 1e-3) / 1e9
+
+
 def cpu_baseline(case, budget_s: float = 15.0):
     """Time the oracle on a prefix sample of the sequences (kind 'port')."""
     import numpy as np
@@ -85,6 +173,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--layout", choices=["NHD", "HND"], default=None,
+                    help="override the configuration's cache layout (same logical data)")
+    ap.add_argument("--partition", type=int, default=None,
+                    help="override the configuration's split-K partition size (tokens; 0 = one partition)")
+    ap.add_argument("--probe", choices=["read", "copy", "gather"], default=None,
+                    help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -103,8 +197,20 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.probe == "gather":
+        for cb in (256, 4096):
+            for per_cu, unroll in ((16, 8), (8, 8), (4, 8), (2, 8), (2, 16), (2, 32), (1, 32)):
+                bw = gather_probe(cb, per_cu=per_cu, unroll=unroll)
+                print(json.dumps({"probe": "gather", "chunk_bytes": cb, "waves_per_cu": per_cu * 4,
+                                  "kib_in_flight_per_wave": unroll, "GB/s": round(bw, 1)}), flush=True)
+        return 0
+    if args.probe:
+        print(json.dumps({"probe": args.probe, "bytes": 4 << 30, "GB/s": round(hbm_probe(args.probe), 1)}))
+        return 0
     log(f"[bench] building config {args.config} inputs")
-    case = workloads.config(args.config, dev)
+    case = workloads.config(args.config, dev, layout=args.layout)
+    if args.partition is not None:
+        case.partition_tokens = args.partition
     out = torch.empty((case.sequences, case.query_heads, case.value_head_size), device=dev, dtype=case.dtype)
     need = ops.extended_workspace_elements(case.sequences, case.query_heads, case.value_head_size,
                                            case.max_sequence_length, case.partition_tokens)
@@ -194,6 +300,8 @@ def main() -> int:
         if t.get("workload") == case.name:
             traffic = t.get("bytes_per_launch")
 
+    peak_read = hbm_probe("read")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
@@ -223,6 +331,8 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "measured_stream_read_gbps": round(peak_read, 1),
+            "frac_of_measured": round(achieved / peak_read, 4),
             "traffic": traffic,
             "kernel": "decode_mfma_kernel",
         },
