@@ -895,6 +895,8 @@ __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, u
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
 }
 
+__device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
+
 template <typename QE, bool kFp8>
 struct StreamDecoder {
   using Ops = MfmaOps<QE>;
@@ -924,9 +926,12 @@ struct StreamDecoder {
 
   // Physical block of the step starting at token t0 (clamped to the last
   // active block, so steps past the sequence stay in valid memory).
+  // The value is ready after the next scalar_ready() on it.
   __device__ __forceinline__ uint32_t block_of(uint32_t t0) const {
     const uint32_t lb = min(t0 >> a.block_shift, last_block);
-    return static_cast<uint32_t>(table[lb]);
+    uint32_t blk;
+    asm volatile("s_load_dword %0, %1, 0x0" : "=s"(blk) : "s"(table + lb));
+    return blk;
   }
 
   __device__ __forceinline__ uint64_t row_base(uint64_t base, uint64_t stride_b, uint64_t stride_p, uint32_t blk,
@@ -1044,8 +1049,9 @@ void decode_stream_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8>;
   using Buf = typename Dec::Buf;
   using vec8 = typename Dec::vec8;
-  __shared__ __attribute__((aligned(16))) uint8_t tile0[kSplit * kStepTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t tile1[kSplit * kStepTileBytes];
+  // Two 4 KiB V tiles per wave; after the loop the same memory holds each
+  // wave's O (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * 2 * kStepTileBytes];
 
   // KV head fastest (see decode_mfma_kernel).
   const uint32_t bid = blockIdx.x;
@@ -1081,9 +1087,9 @@ void decode_stream_kernel(DecodeArgs a) {
     const uint32_t ch = (dec.lane & 15U) ^ (((dec.lane >> 4) & 3U) << 1);
     dec.v_voff = static_cast<uint32_t>((dec.lane >> 4) * dec.vstride_p) + ch * 16;
   }
-  const uint32_t wave = kSplit == 1 ? 0U : (threadIdx.x >> 6);
-  uint8_t* tA = tile0 + wave * kStepTileBytes;
-  uint8_t* tB = tile1 + wave * kStepTileBytes;
+  const uint32_t wave = kSplit == 1 ? 0U : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* tA = tiles + wave * 2 * kStepTileBytes;
+  uint8_t* tB = tA + kStepTileBytes;
 
   float k_scale = 1.0f, v_scale = 1.0f;
   if (kFp8) {
@@ -1130,17 +1136,16 @@ void decode_stream_kernel(DecodeArgs a) {
     uint32_t blk1 = dec.block_of(min(t_first + st, t_last));
     uint32_t nextA = dec.block_of(min(t_first + 2 * st, t_last));
     uint32_t nextB = dec.block_of(min(t_first + 3 * st, t_last));
+    scalar_ready(blk0);
+    scalar_ready(blk1);
     dec.issue(bA, tA, blk0, t_first);
     if (!kFp8) dec.issue_v_dma(tA, blk0, t_first);
     dec.issue(bB, tB, blk1, min(t_first + st, t_last));
     if (!kFp8) dec.issue_v_dma(tB, blk1, min(t_first + st, t_last));
-    for (uint32_t n = 0; n < my_n; ++n) {
-      Buf& b = (n & 1) ? bB : bA;
-      uint8_t* tile = (n & 1) ? tB : tA;
-      uint32_t& next = (n & 1) ? nextB : nextA;
-      const uint32_t t0 = t_first + n * st;
+    auto step = [&](Buf& b, uint8_t* tile, uint32_t& next, uint32_t t0) {
       const uint32_t t2 = min(t0 + 2 * st, t_last);
       vm_wait<L>(b);  // this step's loads; the next step's L stay in flight
+      scalar_ready(next);
       if (kFp8) {
         dec.stage_v_fp8(b, tile, t0);
         wave_fence_lds();
@@ -1168,6 +1173,12 @@ void decode_stream_kernel(DecodeArgs a) {
       }
       wave_fence_lds();
       next = dec.block_of(min(t0 + 4 * st, t_last));
+    };
+    for (uint32_t n = 0; n < my_n; n += 2) {
+      const uint32_t t0 = t_first + n * st;
+      step(bA, tA, nextA, t0);
+      if (n + 1 >= my_n) break;
+      step(bB, tB, nextB, t0 + st);
     }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   }
@@ -1206,11 +1217,10 @@ void decode_stream_kernel(DecodeArgs a) {
     return;
   }
 
-  // Several waves split the partition: reduce through LDS. Each wave's O
-  // [16 heads][128 dims] needs 8 KiB: tile0 and tile1 slots of that wave are
-  // adjacent only per array, so O goes to tile0 (rows 0..7 of 16 heads... )
-  __shared__ float red_o[kSplit][16][kDim];
+  // Several waves split the partition: reduce through LDS.
+  float (*red_o)[16][kDim] = reinterpret_cast<float (*)[16][kDim]>(tiles);
   __shared__ float red_ml[kSplit][16][2];
+  __syncthreads();  // every wave is done with its V tiles
   if (dec.g == 0) {
     red_ml[wave][h][0] = dec.m;
     red_ml[wave][h][1] = l;
@@ -1600,6 +1610,26 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
+template <typename QE, bool kFp8, int kSplit>
+int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
+  TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(kSplit * 64), 0, stream, args);
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
+// The streaming kernel needs steps that stay inside one block (power-of-two
+// block size >= 16, partitions starting on multiples of 16), at most 16 query
+// heads per KV head, and per-lane byte offsets (15 pages + one row) that fit
+// in 31 bits.
+bool stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
+  if (group > 16 || p.block_size < kStep) return false;
+  if (parts > 1 && p.partition_tokens % kStep != 0) return false;
+  const uint64_t es = cache_elem_size(p);
+  const uint64_t limit = 1ULL << 31;
+  return 15 * p.k_page * es + 256 < limit && 15 * p.v_page * es + 256 < limit;
+}
+
 template <typename QE, typename CE>
 int launch_vector(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
@@ -1658,7 +1688,18 @@ int run_typed(const Problem& p, hipStream_t stream) {
       return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
     args.grid_y = p.kv_heads;
     const uint32_t chunks = (partition_tokens + kChunk - 1) / kChunk;
-    if (group > 16) {
+    const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
+    if (stream_eligible(p, parts, group)) {
+      // Waves per workgroup: one when the grid alone fills the chip's 4096
+      // wave slots (16 per CU); otherwise each partition is split over 4
+      // waves when that leaves at least 2 steps per wave. (16-wave groups
+      // measured slower: they add no CUs, only contention within one.)
+      if (grid >= 4096 || steps < 8) {
+        status = fp8 ? launch_stream<QE, true, 1>(args, grid, stream) : launch_stream<QE, false, 1>(args, grid, stream);
+      } else {
+        status = fp8 ? launch_stream<QE, true, 4>(args, grid, stream) : launch_stream<QE, false, 4>(args, grid, stream);
+      }
+    } else if (group > 16) {
       status = fp8 ? launch_mfma_waves<QE, true, 2>(args, grid, chunks, stream)
                    : launch_mfma_waves<QE, false, 2>(args, grid, chunks, stream);
     } else {
@@ -1959,9 +2000,10 @@ int loom_hip_paged_decode_attention_supports(
   if (reason != nullptr) *reason = why;
   if (kernel_family != nullptr) {
     *kernel_family = status != LOOM_HIP_SUCCESS ? ""
-                     : mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
-                         ? "mfma"
-                         : "vector";
+                     : !mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
+                         ? "vector"
+                         : (query_heads / kv_heads <= 16 && block_size >= kStep) ? "mfma-stream"
+                                                                                  : "mfma";
   }
   return status;
 }

@@ -217,8 +217,19 @@ def main() -> int:
     workspace = torch.empty(max(need, 1), device=dev, dtype=torch.float32) if need else None
     kv_bytes = case.kv_bytes()
 
+    # Rotate through copies of the K/V pool so that every timed call reads at
+    # least 1 GiB of distinct KV: a pool smaller than that would be served
+    # partly from the 256 MB Infinity Cache and overstate HBM bandwidth.
+    import dataclasses
+
+    copies = max(1, min(16, -(-(1 << 30) // kv_bytes)))
+    pools = [case] + [dataclasses.replace(case, key_cache=case.key_cache.clone(), value_cache=case.value_cache.clone())
+                      for _ in range(copies - 1)]
+    turn = [0]
+
     def step():
-        workloads.run_case(case, output=out, workspace=workspace)
+        workloads.run_case(pools[turn[0]], output=out, workspace=workspace)
+        turn[0] = (turn[0] + 1) % copies
 
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
@@ -302,6 +313,16 @@ def main() -> int:
 
     peak_read = hbm_probe("read")
 
+    enc = _native.KV_CACHE_FP8_E4M3 if case.cache_encoding == "fp8" else _native.KV_CACHE_NATIVE
+    qdt = {torch.float32: _native.F32, torch.float16: _native.F16, torch.bfloat16: _native.BF16}[case.dtype]
+    _, _, family = ops.supports(qdt, enc, case.sequences, case.query_heads, case.kv_heads, case.head_size,
+                                case.value_head_size, case.num_blocks, case.block_size,
+                                case.max_blocks_per_sequence, case.max_sequence_length, case.scale)
+    if family == "mfma-stream" and case.partition_tokens % 16 != 0:
+        family = "mfma"
+    kernel_name = {"mfma-stream": "decode_stream_kernel", "mfma": "decode_mfma_kernel"}.get(family,
+                                                                                          "decode_vector_kernel")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
@@ -324,7 +345,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16" if case.dtype == torch.bfloat16 else str(case.dtype).replace("torch.", ""),
         "data": "synthetic (seeded N(0,1) Q/K/V rounded to the storage dtype, seeded lengths and shuffled block table)",
-        "config": {**case.describe(), "kv_bytes_per_call": kv_bytes, "parallelism": "none (1 GPU)"},
+        "config": {**case.describe(), "kv_bytes_per_call": kv_bytes, "kv_pool_copies_rotated": copies,
+                   "parallelism": "none (1 GPU)"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
@@ -334,7 +356,7 @@ def main() -> int:
             "measured_stream_read_gbps": round(peak_read, 1),
             "frac_of_measured": round(achieved / peak_read, 4),
             "traffic": traffic,
-            "kernel": "decode_mfma_kernel",
+            "kernel": kernel_name,
         },
         "cpu_baseline": cpu,
     }

@@ -234,8 +234,12 @@ int loom_hip_paged_decode_attention_extended_bf16(
  * attention_dispatch.rs:330-344). Reports without launching work. Returns
  * LOOM_HIP_SUCCESS when the shape is executable, LOOM_HIP_UNSUPPORTED or
  * LOOM_HIP_INVALID_ARGUMENT otherwise, with a static reason in *reason
- * (nullable). *kernel_family (nullable) receives "mfma" for the matrix-core
- * kernel or "vector" for the general kernel.
+ * (nullable). *kernel_family (nullable) receives "mfma-stream" for the
+ * 16-token matrix-core kernel (at most 16 query heads per KV head, block size
+ * >= 16), "mfma" for the 32-token matrix-core kernel or "vector" for the
+ * general kernel. A call whose partition size is not a multiple of 16 moves
+ * from "mfma-stream" to "mfma"; one whose strides or pointers are not 16-byte
+ * aligned moves to "vector".
  */
 int loom_hip_paged_decode_attention_supports(
     uint32_t dtype, uint32_t cache_encoding, uint32_t sequences,

@@ -219,7 +219,7 @@ def test_mfma_and_vector_kernels_agree():
     case = case_from(shape, torch.bfloat16, seed=5)
     s, _, fam = ops.supports(2, 0, 4, 32, 8, 128, 128, case.num_blocks, 16, case.max_blocks_per_sequence, 2048,
                              case.scale)
-    assert fam == "mfma"
+    assert fam == "mfma-stream"
     fast = workloads.run_case(case)
     # Re-home the caches with a block stride of one block + 4 elements.
     NB = case.num_blocks
@@ -241,6 +241,27 @@ def test_mfma_and_vector_kernels_agree():
 # ---------------------------------------------------------------------------
 # Benchmark configurations
 # ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("encoding", ["native", "fp8"])
+@pytest.mark.parametrize("block_size,partition_tokens,family", [
+    (16, 512, "mfma-stream"),   # 16-token steps, one wave per partition
+    (64, 0, "mfma-stream"),     # single partition split over 4 waves, 4 steps per block
+    (16, 520, "mfma"),          # partition not a multiple of 16: 32-token kernel
+    (8, 256, "mfma"),           # block smaller than a 16-token step: 32-token kernel
+])
+def test_matrix_core_kernels_match_oracle(dtype, encoding, block_size, partition_tokens, family):
+    """The two matrix-core kernels on the same data, each against the oracle,
+    with ragged lengths (1, a partial last step, several blocks)."""
+    shape = (4, 32, 8, 128, 128, block_size, [700, 1, 33, 2050])
+    case = case_from(shape, dtype, seed=23, cache_encoding=encoding, layout="NHD",
+                     partition_tokens=partition_tokens)
+    out, lse = workloads.run_case(case, return_lse=True)
+    torch.cuda.synchronize()
+    expected, want_lse = oracle_expected(case)
+    assert_parity(out, expected, dtype, f"{family} bs{block_size} part{partition_tokens} {encoding}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
 def test_config1_f32_plumbing_full():
