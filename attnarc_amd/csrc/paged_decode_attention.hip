@@ -83,6 +83,7 @@ struct DecodeArgs {
   uint32_t parts;  // partitions per (sequence, head); 1 = write output directly
   uint32_t scale_stride;
   uint32_t grid_y;  // decode kernels: work items per sequence besides partitions
+  uint32_t sequences;
   float score_scale_log2;  // scale * log2(e)
 };
 
@@ -883,6 +884,23 @@ __device__ __forceinline__ void vm_wait(StepBuf<true>& b) {
   asm volatile("s_waitcnt vmcnt(%4)" : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.v[0]), "+v"(b.v[1]) : "n"(N) : "memory");
 }
 
+// The same wait, also binding the query registers (loaded before the step).
+template <int N>
+__device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], StepBuf<false>& b) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.k[2]), "+v"(b.k[3])
+               : "n"(N)
+               : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], StepBuf<true>& b) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.v[0]), "+v"(b.v[1])
+               : "n"(N)
+               : "memory");
+}
+
 // Loads with a wave-uniform 64-bit base and a per-lane 32-bit byte offset.
 template <int kImm>
 __device__ __forceinline__ void vm_load16_sv(u32x4& dst, uint32_t voff, uint64_t base) {
@@ -1043,6 +1061,64 @@ struct StreamDecoder {
   }
 };
 
+// Work-item schedule of the streaming kernel. The grid has one workgroup per
+// (sequence, partition, KV head) slot; slots are handed out so that every full
+// partition comes first and the shorter last partitions of the sequences come
+// after them (longest-first, which shortens the tail of a ragged batch), with
+// empty slots at the end. Pairs (sequence, partition) are numbered in sequence
+// order inside each class and the KV head varies fastest, so the heads of one
+// block are read close together in time. Every wave of the workgroup computes
+// the same (wave-uniform) answer from the sequence lengths.
+struct WorkItem {
+  uint32_t seq, part, kvh, len;
+  bool valid;
+};
+
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane) {
+#pragma unroll
+  for (uint32_t d = 1; d < 64; d <<= 1) {
+    const uint32_t t = __shfl_up(x, d, 64);
+    if (lane >= d) x += t;
+  }
+  return x;
+}
+
+__device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t bid) {
+  WorkItem it{0, 0, 0, 0, false};
+  const uint32_t lane = threadIdx.x & 63U;
+  const uint32_t pt = a.partition_tokens;
+  it.kvh = bid % a.kv_heads;
+  const uint32_t pair = bid / a.kv_heads;
+  // Class 0: full partitions (len / pt per sequence); class 1: one partial
+  // last partition per sequence whose length is not a multiple of pt.
+  uint32_t before = 0;  // pairs of earlier classes and chunks
+#pragma unroll 1
+  for (int cls = 0; cls < 2; ++cls) {
+#pragma unroll 1
+    for (uint32_t c0 = 0; c0 < a.sequences; c0 += 64) {
+      const uint32_t s = c0 + lane;
+      const uint32_t len = s < a.sequences ? static_cast<uint32_t>(a.sequence_lengths[s]) : 0U;
+      const uint32_t full = len / pt;
+      const uint32_t n = cls == 0 ? full : (len % pt != 0 ? 1U : 0U);
+      const uint32_t incl = wave_inclusive_sum(n, lane);
+      const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
+      if (pair < before + total) {
+        const uint32_t r = pair - before;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > r);
+        const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(hit));
+        it.seq = c0 + src;
+        it.len = __builtin_amdgcn_readlane(len, src);
+        it.part = cls == 0 ? r - (__builtin_amdgcn_readlane(incl, src) - __builtin_amdgcn_readlane(n, src))
+                           : __builtin_amdgcn_readlane(full, src);
+        it.valid = true;
+        return it;
+      }
+      before += total;
+    }
+  }
+  return it;
+}
+
 template <typename QE, bool kFp8, int kSplit>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_stream_kernel(DecodeArgs a) {
@@ -1053,15 +1129,13 @@ void decode_stream_kernel(DecodeArgs a) {
   // wave's O (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * 2 * kStepTileBytes];
 
-  // KV head fastest (see decode_mfma_kernel).
-  const uint32_t bid = blockIdx.x;
-  const uint32_t kvh = bid % a.kv_heads;
-  const uint32_t rest = bid / a.kv_heads;
-  const uint32_t part = rest % a.parts;
-  const uint32_t seq = rest / a.parts;
-  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const WorkItem item = schedule_item(a, blockIdx.x);
+  if (!item.valid) return;  // uniform across the workgroup
+  const uint32_t kvh = item.kvh;
+  const uint32_t part = item.part;
+  const uint32_t seq = item.seq;
+  const uint32_t len = item.len;
   const uint32_t p0 = part * a.partition_tokens;
-  if (p0 >= len) return;
 
   Dec dec(a);
   dec.lane = threadIdx.x & 63U;
@@ -1109,20 +1183,17 @@ void decode_stream_kernel(DecodeArgs a) {
 
   const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
                          (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group) * kDim;
-  {
+  // Q is loaded after the first two steps' K/V and waited for together with
+  // them, so a wave's start costs one memory round trip, not two.
+  u32x4 qw[4];
+  auto issue_q = [&]() {
     const uint32_t h = min(dec.c, a.group - 1U);
-    u32x4 qw[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
       vm_load16(qw[kc], qrow + h * kDim + dim);
     }
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) asm volatile("s_waitcnt vmcnt(0)" : "+v"(qw[kc]));
-    const bool live = dec.c < a.group;
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
-  }
+  };
   dec.m = -INFINITY;
   dec.lsum = 0.0f;
 #pragma unroll
@@ -1142,6 +1213,13 @@ void decode_stream_kernel(DecodeArgs a) {
     if (!kFp8) dec.issue_v_dma(tA, blk0, t_first);
     dec.issue(bB, tB, blk1, min(t_first + st, t_last));
     if (!kFp8) dec.issue_v_dma(tB, blk1, min(t_first + st, t_last));
+    issue_q();
+    vm_wait_q<0>(qw, bA);
+    {
+      const bool live = dec.c < a.group;
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
+    }
     auto step = [&](Buf& b, uint8_t* tile, uint32_t& next, uint32_t t0) {
       const uint32_t t2 = min(t0 + 2 * st, t_last);
       vm_wait<L>(b);  // this step's loads; the next step's L stay in flight
@@ -1665,6 +1743,7 @@ int run_typed(const Problem& p, hipStream_t stream) {
   args.v_block = p.v_block;
   args.v_page = p.v_page;
   args.v_head = p.v_head;
+  args.sequences = p.sequences;
   args.query_heads = p.query_heads;
   args.kv_heads = p.kv_heads;
   args.group = group;
