@@ -901,6 +901,22 @@ __device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], StepBuf<true>& b) {
                : "memory");
 }
 
+// Step buffer of the all-LDS variant: K and V both arrive by DMA, so no
+// registers are in flight between steps.
+struct NoBuf {
+  static constexpr int kLoads = 8;  // 4 K + 4 V DMA instructions per step
+};
+
+template <int N>
+__device__ __forceinline__ void vm_wait(NoBuf&) {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], NoBuf&) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]) : "n"(N) : "memory");
+}
+
 // Loads with a wave-uniform 64-bit base and a per-lane 32-bit byte offset.
 template <int kImm>
 __device__ __forceinline__ void vm_load16_sv(u32x4& dst, uint32_t voff, uint64_t base) {
@@ -915,12 +931,16 @@ __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, u
 
 __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
 
-template <typename QE, bool kFp8>
+template <typename QE, bool kFp8, bool kKLds>
 struct StreamDecoder {
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
-  using Buf = StepBuf<kFp8>;
+  using Buf = typename std::conditional<kKLds, NoBuf, StepBuf<kFp8>>::type;
+  // Per wave and pipeline stage: a V tile, preceded by a K tile when K also
+  // goes through LDS.
+  static constexpr uint32_t kStageBytes = kKLds ? 2 * kStepTileBytes : kStepTileBytes;
+  static constexpr uint32_t kVOff = kKLds ? kStepTileBytes : 0;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -933,6 +953,7 @@ struct StreamDecoder {
   uint64_t kstride_b, vstride_b, kstride_p, vstride_p;  // byte strides
   uint32_t k_voff;   // lane's K offset: page c, dims (lane >> 4)*8 (16-bit) or *16 (FP8)
   uint32_t v_voff;   // 16-bit: lane's DMA offset within a 4-row group; FP8: page lane >> 2, bytes (lane & 3)*32
+  uint32_t k_dma_voff[4];  // all-LDS variant: lane's K DMA offset for rows 4i..4i+3
   float sl2;
 
   vec8 qb[4];
@@ -971,6 +992,32 @@ struct StreamDecoder {
       vm_load16_sv<128>(b.k[2], k_voff, kb);
       vm_load16_sv<192>(b.k[3], k_voff, kb);
     }
+  }
+
+  // All-LDS K: four 1 KiB DMA loads of four full 256-byte rows each (whole
+  // cache lines per instruction, unlike a register operand layout that takes
+  // 64 bytes of 16 rows). Row r keeps its 16-byte chunk L at position
+  // L ^ (r & 15), so the 16 rows read by one MFMA operand fetch fall in 16
+  // different bank groups.
+  __device__ __forceinline__ void issue_k_dma(uint8_t* ktile, uint32_t blk, uint32_t t0) const {
+    const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vm_load16_lds_sv(k_dma_voff[i], kb + 4 * i * kstride_p, ktile + i * 1024);
+  }
+
+  __device__ __forceinline__ vec8 k_operand_lds(const uint8_t* ktile, int kc) const {
+    const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ c;
+    return *reinterpret_cast<const vec8*>(ktile + c * kTileRowBytes + chunk * 16);
+  }
+
+  __device__ __forceinline__ f32x4 qk_lds(const uint8_t* ktile) const {
+    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    vec8 kop[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) kop[kc] = k_operand_lds(ktile, kc);
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) z = Ops::mma(kop[kc], qb[kc], z);
+    return z;
   }
 
   // 16-bit V: four 1 KiB DMA loads, rows 4i..4i+3 of the tile each.
@@ -1119,15 +1166,19 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   return it;
 }
 
-template <typename QE, bool kFp8, int kSplit>
-__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(4)))
+// kKLds selects the all-LDS variant (16-bit caches): K is DMA'd into LDS as
+// whole rows and read back as the MFMA operand; 16 KiB of LDS per wave. The
+// register variant keeps K in VGPRs (8 KiB of LDS per wave, 4 waves per SIMD).
+template <typename QE, bool kFp8, int kSplit, bool kKLds>
+__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(kKLds ? 2 : 4)))
 void decode_stream_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8>;
+  using Dec = StreamDecoder<QE, kFp8, kKLds>;
   using Buf = typename Dec::Buf;
   using vec8 = typename Dec::vec8;
-  // Two 4 KiB V tiles per wave; after the loop the same memory holds each
+  static_assert(!(kKLds && kFp8), "the all-LDS variant reads 16-bit caches");
+  // Two pipeline stages per wave; after the loop the same memory holds each
   // wave's O (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * 2 * kStepTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * 2 * Dec::kStageBytes];
 
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
@@ -1161,9 +1212,16 @@ void decode_stream_kernel(DecodeArgs a) {
     const uint32_t ch = (dec.lane & 15U) ^ (((dec.lane >> 4) & 3U) << 1);
     dec.v_voff = static_cast<uint32_t>((dec.lane >> 4) * dec.vstride_p) + ch * 16;
   }
+  if (kKLds) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = 4 * i + (dec.lane >> 4);
+      dec.k_dma_voff[i] = static_cast<uint32_t>((dec.lane >> 4) * dec.kstride_p) + (((dec.lane & 15U) ^ row) << 4);
+    }
+  }
   const uint32_t wave = kSplit == 1 ? 0U : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* tA = tiles + wave * 2 * kStepTileBytes;
-  uint8_t* tB = tA + kStepTileBytes;
+  uint8_t* tA = tiles + wave * 2 * Dec::kStageBytes;
+  uint8_t* tB = tA + Dec::kStageBytes;
 
   float k_scale = 1.0f, v_scale = 1.0f;
   if (kFp8) {
@@ -1209,10 +1267,17 @@ void decode_stream_kernel(DecodeArgs a) {
     uint32_t nextB = dec.block_of(min(t_first + 3 * st, t_last));
     scalar_ready(blk0);
     scalar_ready(blk1);
-    dec.issue(bA, tA, blk0, t_first);
-    if (!kFp8) dec.issue_v_dma(tA, blk0, t_first);
-    dec.issue(bB, tB, blk1, min(t_first + st, t_last));
-    if (!kFp8) dec.issue_v_dma(tB, blk1, min(t_first + st, t_last));
+    if constexpr (kKLds) {
+      dec.issue_k_dma(tA, blk0, t_first);
+      dec.issue_v_dma(tA + Dec::kVOff, blk0, t_first);
+      dec.issue_k_dma(tB, blk1, min(t_first + st, t_last));
+      dec.issue_v_dma(tB + Dec::kVOff, blk1, min(t_first + st, t_last));
+    } else {
+      dec.issue(bA, tA, blk0, t_first);
+      if (!kFp8) dec.issue_v_dma(tA, blk0, t_first);
+      dec.issue(bB, tB, blk1, min(t_first + st, t_last));
+      if (!kFp8) dec.issue_v_dma(tB, blk1, min(t_first + st, t_last));
+    }
     issue_q();
     vm_wait_q<0>(qw, bA);
     {
@@ -1224,7 +1289,19 @@ void decode_stream_kernel(DecodeArgs a) {
       const uint32_t t2 = min(t0 + 2 * st, t_last);
       vm_wait<L>(b);  // this step's loads; the next step's L stay in flight
       scalar_ready(next);
-      if (kFp8) {
+      if constexpr (kKLds) {
+        uint8_t* vtile = tile + Dec::kVOff;
+        dec.zero_dead_rows(vtile, t0);
+        wave_fence_lds();
+        const f32x4 s = dec.qk_lds(tile);
+        dec.softmax_pv(s, t0, vtile);
+        wait_lds_reads();
+        dec.issue_k_dma(tile, next, t2);
+        dec.issue_v_dma(vtile, next, t2);
+        wave_fence_lds();
+        next = dec.block_of(min(t0 + 4 * st, t_last));
+      } else {
+      if constexpr (kFp8) {
         dec.stage_v_fp8(b, tile, t0);
         wave_fence_lds();
         const uint64_t vb = dec.row_base(dec.vbase, dec.vstride_b, dec.vstride_p, next, t2);
@@ -1251,6 +1328,7 @@ void decode_stream_kernel(DecodeArgs a) {
       }
       wave_fence_lds();
       next = dec.block_of(min(t0 + 4 * st, t_last));
+      }
     };
     for (uint32_t n = 0; n < my_n; n += 2) {
       const uint32_t t0 = t_first + n * st;
@@ -1691,7 +1769,9 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
 template <typename QE, bool kFp8, int kSplit>
 int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit>), dim3(static_cast<uint32_t>(grid)),
+  // 16-bit caches take the all-LDS variant (whole-row loads for K as for V).
+  constexpr bool kKLds = !kFp8;
+  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit, kKLds>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kSplit * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
