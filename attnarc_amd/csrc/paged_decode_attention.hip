@@ -1130,6 +1130,34 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane
   return x;
 }
 
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+
+// Lengths of sequences c0 .. c0 + 63, lane i holding sequence c0 + i (zero
+// past the end). They are read through the scalar cache with bounds-checked
+// buffer loads: a wave that has just started would wait far longer for a
+// vector load queued behind the running waves' KV traffic.
+__device__ __forceinline__ uint32_t lengths_chunk(const DecodeArgs& a, uint32_t c0, uint32_t lane) {
+  const uint64_t base = reinterpret_cast<uint64_t>(a.sequence_lengths);
+  typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
+  const u32x4s rsrc = {static_cast<uint32_t>(base), static_cast<uint32_t>(base >> 32) & 0xFFFFU, a.sequences * 4U,
+                       0x00020000U};
+  u32x16 w0, w1, w2, w3;
+  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w0) : "s"(rsrc), "s"(c0 * 4U));
+  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w1) : "s"(rsrc), "s"(c0 * 4U + 64U));
+  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w2) : "s"(rsrc), "s"(c0 * 4U + 128U));
+  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w3) : "s"(rsrc), "s"(c0 * 4U + 192U));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(w0), "+s"(w1), "+s"(w2), "+s"(w3));
+  uint32_t v = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(w0[i]), "n"(i));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(w1[i]), "n"(16 + i));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(w2[i]), "n"(32 + i));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(w3[i]), "n"(48 + i));
+  }
+  return c0 + lane < a.sequences ? v : 0U;
+}
+
 __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t bid) {
   WorkItem it{0, 0, 0, 0, false};
   const uint32_t lane = threadIdx.x & 63U;
@@ -1143,8 +1171,7 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   for (int cls = 0; cls < 2; ++cls) {
 #pragma unroll 1
     for (uint32_t c0 = 0; c0 < a.sequences; c0 += 64) {
-      const uint32_t s = c0 + lane;
-      const uint32_t len = s < a.sequences ? static_cast<uint32_t>(a.sequence_lengths[s]) : 0U;
+      const uint32_t len = lengths_chunk(a, c0, lane);
       const uint32_t full = len / pt;
       const uint32_t n = cls == 0 ? full : (len % pt != 0 ? 1U : 0U);
       const uint32_t incl = wave_inclusive_sum(n, lane);
@@ -1169,7 +1196,7 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
 // kKLds selects the all-LDS variant (16-bit caches): K is DMA'd into LDS as
 // whole rows and read back as the MFMA operand; 16 KiB of LDS per wave. The
 // register variant keeps K in VGPRs (8 KiB of LDS per wave, 4 waves per SIMD).
-template <typename QE, bool kFp8, int kSplit, bool kKLds>
+template <typename QE, bool kFp8, int kSplit, bool kKLds, int kStages = 2>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(kKLds ? 2 : 4)))
 void decode_stream_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8, kKLds>;
@@ -1178,7 +1205,8 @@ void decode_stream_kernel(DecodeArgs a) {
   static_assert(!(kKLds && kFp8), "the all-LDS variant reads 16-bit caches");
   // Two pipeline stages per wave; after the loop the same memory holds each
   // wave's O (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * 2 * Dec::kStageBytes];
+  static_assert(kStages == 2 || kKLds, "the register variant is double-buffered");
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * kStages * Dec::kStageBytes];
 
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
@@ -1220,7 +1248,7 @@ void decode_stream_kernel(DecodeArgs a) {
     }
   }
   const uint32_t wave = kSplit == 1 ? 0U : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* tA = tiles + wave * 2 * Dec::kStageBytes;
+  uint8_t* tA = tiles + wave * kStages * Dec::kStageBytes;
   uint8_t* tB = tA + Dec::kStageBytes;
 
   float k_scale = 1.0f, v_scale = 1.0f;
@@ -1257,7 +1285,63 @@ void decode_stream_kernel(DecodeArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) dec.acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  if (my_n > 0) {
+  if constexpr (kKLds) {
+    if (my_n > 0) {
+      // kStages steps in flight. Block IDs run kStages steps ahead of the
+      // loads that use them; the issue pattern is uniform (steps past the
+      // wave's last one are clamped onto it).
+      constexpr int S = kStages;
+      NoBuf nb;
+      uint8_t* tl[S];
+      uint32_t nx[S];
+      uint32_t bk[S];
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        tl[i] = tA + i * Dec::kStageBytes;
+        bk[i] = dec.block_of(min(t_first + i * st, t_last));
+      }
+#pragma unroll
+      for (int i = 0; i < S; ++i) nx[i] = dec.block_of(min(t_first + (S + i) * st, t_last));
+#pragma unroll
+      for (int i = 0; i < S; ++i) scalar_ready(bk[i]);
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const uint32_t ti = min(t_first + i * st, t_last);
+        dec.issue_k_dma(tl[i], bk[i], ti);
+        dec.issue_v_dma(tl[i] + Dec::kVOff, bk[i], ti);
+      }
+      issue_q();
+      vm_wait_q<0>(qw, nb);
+      {
+        const bool live = dec.c < a.group;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
+      }
+      for (uint32_t n = 0; n < my_n; n += S) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          if (n + i < my_n) {
+            const uint32_t t0 = t_first + (n + i) * st;
+            const uint32_t tn = min(t0 + S * st, t_last);
+            uint8_t* ktile = tl[i];
+            uint8_t* vtile = tl[i] + Dec::kVOff;
+            vm_wait<NoBuf::kLoads * (S - 1)>(nb);  // this step's loads; S - 1 steps stay in flight
+            scalar_ready(nx[i]);
+            dec.zero_dead_rows(vtile, t0);
+            wave_fence_lds();
+            const f32x4 sc = dec.qk_lds(ktile);
+            dec.softmax_pv(sc, t0, vtile);
+            wait_lds_reads();
+            dec.issue_k_dma(ktile, nx[i], tn);
+            dec.issue_v_dma(vtile, nx[i], tn);
+            wave_fence_lds();
+            nx[i] = dec.block_of(min(t0 + 2 * S * st, t_last));
+          }
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    }
+  } else if (my_n > 0) {
     constexpr int L = Buf::kLoads;
     Buf bA, bB;
     // Block IDs run two steps ahead of the loads that use them.
