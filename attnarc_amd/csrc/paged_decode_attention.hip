@@ -1498,19 +1498,79 @@ void decode_stream_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K merge: one workgroup of 256 threads per (sequence, query head) row.
+// Split-K merge for at most kMergeRowParts partitions (the log-sum-exp
+// identity of paged_decode_attention.cu:780-852): one wave per (sequence,
+// query head) row, four rows per workgroup, no barriers. Only the
+// ceil(len / partition_tokens) partitions that hold tokens are read. Every
+// load of the row (m, l of lane p; two output dims of all partitions per
+// lane) is issued before any result is needed, so a row costs one memory
+// round trip; factors 2^(m_p - M) are broadcast with readlane.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kMergeThreads = 256;
+constexpr uint32_t kMergeRowsPerGroup = kMergeThreads / 64;
+constexpr uint32_t kMergeRowParts = 32;  // largest kParts instantiated
+
+template <typename QE, uint32_t kParts>
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint32_t rows) {
+  using QT = typename QE::T;
+  const uint32_t lane = threadIdx.x & 63U;
+  const uint32_t row = blockIdx.x * kMergeRowsPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint32_t seq = row / a.query_heads;
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const uint32_t n = min(min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts), kParts);
+  const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
+  const float* os = a.ws_o + static_cast<uint64_t>(row) * a.parts * a.value_head_size;
+  const uint32_t Dv = a.value_head_size;
+  QT* out = static_cast<QT*>(a.output) + static_cast<uint64_t>(row) * Dv;
+
+  const float mp = lane < n ? ml[2 * lane] : -INFINITY;
+  const float lp = lane < n ? ml[2 * lane + 1] : 0.0f;
+  for (uint32_t d0 = 0; d0 < Dv; d0 += 128) {
+    const uint32_t d = d0 + 2 * lane;
+    float v0[kParts], v1[kParts];
+#pragma unroll
+    for (uint32_t j = 0; j < kParts; ++j) {
+      const float* src = os + static_cast<uint64_t>(j) * Dv + d;
+      v0[j] = j < n && d < Dv ? src[0] : 0.0f;
+      v1[j] = j < n && d + 1 < Dv ? src[1] : 0.0f;
+    }
+    float M = mp;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    // A partition without tokens would hold m = -inf and contributes nothing.
+    const float f = isfinite(mp) ? exp2f(mp - M) : 0.0f;
+    float L = lp * f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < kParts; ++j) {
+      const float fj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), j));
+      o0 = fmaf(v0[j], fj, o0);
+      o1 = fmaf(v1[j], fj, o1);
+    }
+    const float inv = 1.0f / L;
+    if (d < Dv) out[d] = QE::from_f(o0 * inv);
+    if (d + 1 < Dv) out[d + 1] = QE::from_f(o1 * inv);
+    if (d0 == 0 && lane == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K merge for many partitions: one workgroup of 256 threads per
+// (sequence, query head) row.
 // Only the ceil(len / partition_tokens) partitions that hold tokens are read.
 // Factors f_p = 2^(m_p - M) go to LDS; then wave w accumulates partitions
 // p = w mod 4 for 2 dims per lane (unrolled for loads in flight), and the
 // four partial sums are added in LDS.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kMergeThreads = 256;
 constexpr uint32_t kMergeWaves = kMergeThreads / 64;
 constexpr uint32_t kMergeWindow = 2048;
 constexpr uint32_t kMergeDimsPerPass = 128;
 
 template <typename QE>
-__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a) {
   using QT = typename QE::T;
   __shared__ float factor[kMergeWindow];
   __shared__ float red[kMergeWaves];
@@ -1830,7 +1890,16 @@ uint32_t log2u(uint32_t v) {
 template <typename QE>
 int launch_merge(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_MERGE, stream);
-  hipLaunchKernelGGL(merge_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
+  const dim3 grid((rows + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup);
+  if (args.parts <= 8) {
+    hipLaunchKernelGGL((merge_kernel<QE, 8>), grid, dim3(kMergeThreads), 0, stream, args, rows);
+  } else if (args.parts <= 16) {
+    hipLaunchKernelGGL((merge_kernel<QE, 16>), grid, dim3(kMergeThreads), 0, stream, args, rows);
+  } else if (args.parts <= kMergeRowParts) {
+    hipLaunchKernelGGL((merge_kernel<QE, kMergeRowParts>), grid, dim3(kMergeThreads), 0, stream, args, rows);
+  } else {
+    hipLaunchKernelGGL(merge_wide_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
+  }
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
