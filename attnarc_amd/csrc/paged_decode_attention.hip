@@ -846,81 +846,40 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
 }
 
 // ---------------------------------------------------------------------------
-// Streaming matrix-core kernel: 16-token steps, four waves per SIMD.
+// Streaming matrix-core kernel: 16-token steps, K and V through LDS.
 //
-// Measured on MI355X, a random paged read reaches ~5.8 TB/s only with ~32
-// waves per CU; with 8 waves per CU it stays near 3.2 TB/s however many bytes
-// each wave keeps in flight. This kernel is therefore sized for 16 waves per
-// CU: each wave keeps two 16-token steps in flight with K in registers
-// (2 x 16 VGPRs) and V DMA'd into two 4 KiB LDS tiles, and stays within 128
-// VGPRs. It applies when the block size is a power of two >= 16 and steps are
-// aligned to 16 tokens, so each step lies in one block: the block ID is a
-// scalar load, the row base is scalar arithmetic, and every load uses a
-// loop-invariant per-lane 32-bit offset from that scalar base.
+// Each wave owns one (sequence, split-K partition, KV head) work item (or a
+// quarter of one, when 4 waves split a partition) and walks it in 16-token
+// steps with two steps in flight. It applies when the block size is a power
+// of two >= 16 and partitions start on multiples of 16 tokens, so a step lies
+// in one block: the block ID is one scalar load, the row base is scalar
+// arithmetic, and each load is a global_load_lds_dwordx4 at a loop-invariant
+// 32-bit lane offset from that base.
+//
+// The loads bring whole cache rows: each DMA instruction copies four full
+// 256-byte rows (16-bit) or eight full 128-byte rows (FP8) of the wave's KV
+// head into LDS. Measured on MI355X, this sustains ~11% more HBM bandwidth
+// than loads shaped like the MFMA register operand (64 bytes of 16 rows per
+// instruction). 16-byte chunks are XOR-swizzled by row so that operand reads
+// are bank-conflict free.
 //
 // Per step: QK^T with v_mfma_f32_16x16x32 (S[token 4g + r][head c] lands in
 // lane (g, c)); PV with v_mfma_f32_16x16x16, whose B operand is exactly that
 // S layout (4 tokens of lane group g) and whose A operand (dims dt*16 + c of
-// tokens 4g + k) is one ds_read_b64_tr_b16.
+// tokens 4g + k) is one ds_read_b64_tr_b16 from the 16-bit V tile. FP8 V is
+// converted into that tile once per step; FP8 K is converted as it is read.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kStep = 16;
 constexpr uint32_t kStepTileBytes = kStep * kTileRowBytes;  // 4 KiB
 
-template <bool kFp8>
-struct StepBuf {
-  static constexpr int kK = kFp8 ? 2 : 4;      // 16-byte K loads per lane
-  static constexpr int kLoads = kFp8 ? 4 : 8;  // vector-memory instructions per step
-  u32x4 k[kK];
-  u32x4 v[2];  // FP8 V (16-bit V goes to LDS by DMA)
-};
-
 template <int N>
-__device__ __forceinline__ void vm_wait(StepBuf<false>& b) {
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.k[2]), "+v"(b.k[3]) : "n"(N) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void vm_wait(StepBuf<true>& b) {
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.v[0]), "+v"(b.v[1]) : "n"(N) : "memory");
-}
-
-// The same wait, also binding the query registers (loaded before the step).
-template <int N>
-__device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], StepBuf<false>& b) {
-  asm volatile("s_waitcnt vmcnt(%8)"
-               : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.k[2]), "+v"(b.k[3])
-               : "n"(N)
-               : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], StepBuf<true>& b) {
-  asm volatile("s_waitcnt vmcnt(%8)"
-               : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(b.k[0]), "+v"(b.k[1]), "+v"(b.v[0]), "+v"(b.v[1])
-               : "n"(N)
-               : "memory");
-}
-
-// Step buffer of the all-LDS variant: K and V both arrive by DMA, so no
-// registers are in flight between steps.
-struct NoBuf {
-  static constexpr int kLoads = 8;  // 4 K + 4 V DMA instructions per step
-};
-
-template <int N>
-__device__ __forceinline__ void vm_wait(NoBuf&) {
+__device__ __forceinline__ void vm_wait_dma() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
-template <int N>
-__device__ __forceinline__ void vm_wait_q(u32x4 (&q)[4], NoBuf&) {
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]) : "n"(N) : "memory");
-}
-
-// Loads with a wave-uniform 64-bit base and a per-lane 32-bit byte offset.
-template <int kImm>
-__device__ __forceinline__ void vm_load16_sv(u32x4& dst, uint32_t voff, uint64_t base) {
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(dst) : "v"(voff), "s"(base), "n"(kImm));
+// Waits for the query registers as well (loaded after the K/V DMA).
+__device__ __forceinline__ void vm_wait_all(u32x4 (&q)[4]) {
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]) : : "memory");
 }
 
 __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, uint8_t* lds) {
@@ -931,16 +890,17 @@ __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, u
 
 __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
 
-template <typename QE, bool kFp8, bool kKLds>
+template <typename QE, bool kFp8>
 struct StreamDecoder {
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
-  using Buf = typename std::conditional<kKLds, NoBuf, StepBuf<kFp8>>::type;
-  // Per wave and pipeline stage: a V tile, preceded by a K tile when K also
-  // goes through LDS.
-  static constexpr uint32_t kStageBytes = kKLds ? 2 * kStepTileBytes : kStepTileBytes;
-  static constexpr uint32_t kVOff = kKLds ? kStepTileBytes : 0;
+  // Stage layout per wave. 16-bit: [K 4 KiB | V 4 KiB]. FP8: [K bytes 2 KiB |
+  // V bytes 2 KiB | V as 16 bits 4 KiB]. kVOff locates the 16-bit V tile.
+  static constexpr uint32_t kStageBytes = 2 * kStepTileBytes;
+  static constexpr uint32_t kF8TileBytes = kStep * kDim;  // 2 KiB
+  static constexpr uint32_t kVOff = kFp8 ? 2 * kF8TileBytes : kStepTileBytes;
+  static constexpr int kDmaPerStep = kFp8 ? 4 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -951,9 +911,9 @@ struct StreamDecoder {
   const int32_t* table;
   uint64_t kbase, vbase;  // byte address of (block 0, page 0, this kv head)
   uint64_t kstride_b, vstride_b, kstride_p, vstride_p;  // byte strides
-  uint32_t k_voff;   // lane's K offset: page c, dims (lane >> 4)*8 (16-bit) or *16 (FP8)
-  uint32_t v_voff;   // 16-bit: lane's DMA offset within a 4-row group; FP8: page lane >> 2, bytes (lane & 3)*32
-  uint32_t k_dma_voff[4];  // all-LDS variant: lane's K DMA offset for rows 4i..4i+3
+  uint32_t k_voff[4];  // 16-bit: lane's K DMA offset for rows 4i..4i+3
+  uint32_t v_voff;     // 16-bit: lane's V DMA offset within a 4-row group
+  uint32_t f8_k_voff, f8_v_voff;  // FP8: lane's K / V DMA offsets within 8 rows
   float sl2;
 
   vec8 qb[4];
@@ -978,64 +938,79 @@ struct StreamDecoder {
     return base + blk * stride_b + (t0 & (a.block_size - 1U)) * stride_p;
   }
 
-  __device__ __forceinline__ void issue(Buf& b, uint8_t* tile, uint32_t blk, uint32_t t0) const {
-    const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
-    const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
+  // Lane DMA offsets. 16-bit K: instruction i brings rows 4i + lane / 16;
+  // row r keeps its 16-byte chunk L at position L ^ (r & 15), so the 16 rows
+  // of one MFMA operand fetch fall in different bank groups. 16-bit V: chunk
+  // L of row r at L ^ 2 (r & 3), which the transposed reads need. FP8: eight
+  // 128-byte rows per instruction, chunk L of row r at L ^ (r & 7).
+  __device__ __forceinline__ void init_offsets() {
     if (kFp8) {
-      vm_load16_sv<0>(b.v[0], v_voff, vb);
-      vm_load16_sv<16>(b.v[1], v_voff, vb);
-      vm_load16_sv<0>(b.k[0], k_voff, kb);
-      vm_load16_sv<64>(b.k[1], k_voff, kb);
+      const uint32_t row = lane >> 3;
+      const uint32_t chunk = ((lane & 7U) ^ (row & 7U)) << 4;
+      f8_k_voff = static_cast<uint32_t>(row * kstride_p) + chunk;
+      f8_v_voff = static_cast<uint32_t>(row * vstride_p) + chunk;
     } else {
-      vm_load16_sv<0>(b.k[0], k_voff, kb);
-      vm_load16_sv<64>(b.k[1], k_voff, kb);
-      vm_load16_sv<128>(b.k[2], k_voff, kb);
-      vm_load16_sv<192>(b.k[3], k_voff, kb);
+      const uint32_t row = lane >> 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        k_voff[i] = static_cast<uint32_t>(row * kstride_p) + (((lane & 15U) ^ (4 * i + row)) << 4);
+      v_voff = static_cast<uint32_t>(row * vstride_p) + (((lane & 15U) ^ ((row & 3U) << 1)) << 4);
     }
   }
 
-  // All-LDS K: four 1 KiB DMA loads of four full 256-byte rows each (whole
-  // cache lines per instruction, unlike a register operand layout that takes
-  // 64 bytes of 16 rows). Row r keeps its 16-byte chunk L at position
-  // L ^ (r & 15), so the 16 rows read by one MFMA operand fetch fall in 16
-  // different bank groups.
-  __device__ __forceinline__ void issue_k_dma(uint8_t* ktile, uint32_t blk, uint32_t t0) const {
+  // One step's K and V (and nothing else) into a stage.
+  __device__ __forceinline__ void issue(uint8_t* stage, uint32_t blk, uint32_t t0) const {
     const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
+    const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
+    if (kFp8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vm_load16_lds_sv(k_dma_voff[i], kb + 4 * i * kstride_p, ktile + i * 1024);
+      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff, kb + 8 * i * kstride_p, stage + i * 1024);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_v_voff, vb + 8 * i * vstride_p, stage + kF8TileBytes + i * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(k_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(v_voff, vb + 4 * i * vstride_p, stage + kVOff + i * 1024);
+    }
   }
 
-  __device__ __forceinline__ vec8 k_operand_lds(const uint8_t* ktile, int kc) const {
-    const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ c;
-    return *reinterpret_cast<const vec8*>(ktile + c * kTileRowBytes + chunk * 16);
+  // MFMA A operand kc of token c. 16-bit: dims kc*32 + g*8 .. +7. FP8: dims
+  // (kc >> 1)*64 + g*16 + (kc & 1)*8 .. +7, converted (Q uses the same dims).
+  __device__ __forceinline__ vec8 k_operand(const uint8_t* stage, int kc) const {
+    if (kFp8) {
+      const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ (c & 7U);
+      const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kDim + chunk * 16 + (kc & 1) * 8);
+      return Ops::from_fp8(w.x, w.y);
+    } else {
+      const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ c;
+      return *reinterpret_cast<const vec8*>(stage + c * kTileRowBytes + chunk * 16);
+    }
   }
 
-  __device__ __forceinline__ f32x4 qk_lds(const uint8_t* ktile) const {
+  __device__ __forceinline__ f32x4 qk(const uint8_t* stage) const {
     f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
     vec8 kop[4];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) kop[kc] = k_operand_lds(ktile, kc);
+    for (int kc = 0; kc < 4; ++kc) kop[kc] = k_operand(stage, kc);
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) z = Ops::mma(kop[kc], qb[kc], z);
     return z;
   }
 
-  // 16-bit V: four 1 KiB DMA loads, rows 4i..4i+3 of the tile each.
-  __device__ __forceinline__ void issue_v_dma(uint8_t* tile, uint32_t blk, uint32_t t0) const {
-    const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) vm_load16_lds_sv(v_voff, vb + 4 * i * vstride_p, tile + i * 1024);
-  }
-
-  // FP8 V: 32 bytes of token lane >> 2 -> 32 16-bit values (rows past the
-  // sequence end become zero), four 16-byte chunks of the tile row.
-  __device__ __forceinline__ void stage_v_fp8(const Buf& b, uint8_t* tile, uint32_t t0) const {
+  // FP8 V bytes -> the swizzled 16-bit V tile: lane handles 32 bytes of token
+  // lane >> 2 (rows past the sequence end become zero).
+  __device__ __forceinline__ void stage_v_fp8(uint8_t* stage, uint32_t t0) const {
     const uint32_t t = lane >> 2;
     const bool live = t0 + t < len;
+    const uint8_t* vrow = stage + kF8TileBytes + t * kDim;
+    uint8_t* tile = stage + kVOff;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const u32x4 w = live ? b.v[h] : u32x4{0U, 0U, 0U, 0U};
-      const uint32_t ch = (lane & 3U) * 4 + h * 2;
+      const uint32_t lc = (lane & 3U) * 2 + h;  // logical 16-byte chunk of the FP8 row
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ (t & 7U)) << 4));
+      const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
+      const uint32_t ch = lc * 2;  // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each)
       *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = Ops::from_fp8(w[0], w[1]);
       *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = Ops::from_fp8(w[2], w[3]);
     }
@@ -1051,22 +1026,6 @@ struct StreamDecoder {
 #pragma unroll
       for (int i = 0; i < 4; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
     }
-  }
-
-  __device__ __forceinline__ vec8 k_operand(const Buf& b, int kc) const {
-    if (kFp8) {
-      const u32x4 w = b.k[kc >> 1];
-      return (kc & 1) ? Ops::from_fp8(w[2], w[3]) : Ops::from_fp8(w[0], w[1]);
-    } else {
-      return __builtin_bit_cast(vec8, b.k[kc]);
-    }
-  }
-
-  __device__ __forceinline__ f32x4 qk(const Buf& b) const {
-    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) z = Ops::mma(k_operand(b, kc), qb[kc], z);
-    return z;
   }
 
   __device__ __forceinline__ void softmax_pv(f32x4 s, uint32_t t0, const uint8_t* tile) {
@@ -1193,20 +1152,15 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   return it;
 }
 
-// kKLds selects the all-LDS variant (16-bit caches): K is DMA'd into LDS as
-// whole rows and read back as the MFMA operand; 16 KiB of LDS per wave. The
-// register variant keeps K in VGPRs (8 KiB of LDS per wave, 4 waves per SIMD).
-template <typename QE, bool kFp8, int kSplit, bool kKLds, int kStages = 2>
-__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(kKLds ? 2 : 4)))
+template <typename QE, bool kFp8, int kSplit>
+__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8, kKLds>;
-  using Buf = typename Dec::Buf;
+  using Dec = StreamDecoder<QE, kFp8>;
   using vec8 = typename Dec::vec8;
-  static_assert(!(kKLds && kFp8), "the all-LDS variant reads 16-bit caches");
-  // Two pipeline stages per wave; after the loop the same memory holds each
-  // wave's O (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
-  static_assert(kStages == 2 || kKLds, "the register variant is double-buffered");
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * kStages * Dec::kStageBytes];
+  constexpr int S = 2;  // pipeline stages (deeper pipelines measured no faster)
+  // S stages per wave; after the loop the same memory holds each wave's O
+  // (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * S * Dec::kStageBytes];
 
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
@@ -1231,25 +1185,9 @@ void decode_stream_kernel(DecodeArgs a) {
   dec.vstride_p = a.v_page * es;
   dec.kbase = reinterpret_cast<uint64_t>(a.key_cache) + static_cast<uint64_t>(kvh) * a.k_head * es;
   dec.vbase = reinterpret_cast<uint64_t>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head * es;
-  dec.k_voff = static_cast<uint32_t>(dec.c * dec.kstride_p) + (kFp8 ? dec.g * 16 : dec.g * 16);
-  if (kFp8) {
-    dec.v_voff = static_cast<uint32_t>((dec.lane >> 2) * dec.vstride_p) + (dec.lane & 3U) * 32;
-  } else {
-    // DMA slot of lane l in a 4-row group: row l >> 4, physical chunk l & 15,
-    // which holds logical chunk (l & 15) ^ 2*(row & 3).
-    const uint32_t ch = (dec.lane & 15U) ^ (((dec.lane >> 4) & 3U) << 1);
-    dec.v_voff = static_cast<uint32_t>((dec.lane >> 4) * dec.vstride_p) + ch * 16;
-  }
-  if (kKLds) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t row = 4 * i + (dec.lane >> 4);
-      dec.k_dma_voff[i] = static_cast<uint32_t>((dec.lane >> 4) * dec.kstride_p) + (((dec.lane & 15U) ^ row) << 4);
-    }
-  }
+  dec.init_offsets();
   const uint32_t wave = kSplit == 1 ? 0U : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* tA = tiles + wave * kStages * Dec::kStageBytes;
-  uint8_t* tB = tA + Dec::kStageBytes;
+  uint8_t* tw = tiles + wave * S * Dec::kStageBytes;
 
   float k_scale = 1.0f, v_scale = 1.0f;
   if (kFp8) {
@@ -1267,158 +1205,67 @@ void decode_stream_kernel(DecodeArgs a) {
   const uint32_t t_first = p0 + wave * kStep;
   const uint32_t t_last = t_first + (my_n > 0 ? my_n - 1 : 0) * st;
 
-  const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
-                         (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group) * kDim;
-  // Q is loaded after the first two steps' K/V and waited for together with
-  // them, so a wave's start costs one memory round trip, not two.
-  u32x4 qw[4];
-  auto issue_q = [&]() {
-    const uint32_t h = min(dec.c, a.group - 1U);
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
-      vm_load16(qw[kc], qrow + h * kDim + dim);
-    }
-  };
   dec.m = -INFINITY;
   dec.lsum = 0.0f;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) dec.acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  if constexpr (kKLds) {
-    if (my_n > 0) {
-      // kStages steps in flight. Block IDs run kStages steps ahead of the
-      // loads that use them; the issue pattern is uniform (steps past the
-      // wave's last one are clamped onto it).
-      constexpr int S = kStages;
-      NoBuf nb;
-      uint8_t* tl[S];
-      uint32_t nx[S];
-      uint32_t bk[S];
+  if (my_n > 0) {
+    // Block IDs run S steps ahead of the loads that use them.
+    uint8_t* tl[S];
+    uint32_t nx[S];
+    uint32_t bk[S];
 #pragma unroll
-      for (int i = 0; i < S; ++i) {
-        tl[i] = tA + i * Dec::kStageBytes;
-        bk[i] = dec.block_of(min(t_first + i * st, t_last));
-      }
-#pragma unroll
-      for (int i = 0; i < S; ++i) nx[i] = dec.block_of(min(t_first + (S + i) * st, t_last));
-#pragma unroll
-      for (int i = 0; i < S; ++i) scalar_ready(bk[i]);
-#pragma unroll
-      for (int i = 0; i < S; ++i) {
-        const uint32_t ti = min(t_first + i * st, t_last);
-        dec.issue_k_dma(tl[i], bk[i], ti);
-        dec.issue_v_dma(tl[i] + Dec::kVOff, bk[i], ti);
-      }
-      issue_q();
-      vm_wait_q<0>(qw, nb);
-      {
-        const bool live = dec.c < a.group;
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
-      }
-      for (uint32_t n = 0; n < my_n; n += S) {
-#pragma unroll
-        for (int i = 0; i < S; ++i) {
-          if (n + i < my_n) {
-            const uint32_t t0 = t_first + (n + i) * st;
-            const uint32_t tn = min(t0 + S * st, t_last);
-            uint8_t* ktile = tl[i];
-            uint8_t* vtile = tl[i] + Dec::kVOff;
-            vm_wait<NoBuf::kLoads * (S - 1)>(nb);  // this step's loads; S - 1 steps stay in flight
-            scalar_ready(nx[i]);
-            dec.zero_dead_rows(vtile, t0);
-            wave_fence_lds();
-            const f32x4 sc = dec.qk_lds(ktile);
-            dec.softmax_pv(sc, t0, vtile);
-            wait_lds_reads();
-            dec.issue_k_dma(ktile, nx[i], tn);
-            dec.issue_v_dma(vtile, nx[i], tn);
-            wave_fence_lds();
-            nx[i] = dec.block_of(min(t0 + 2 * S * st, t_last));
-          }
-        }
-      }
-      asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    for (int i = 0; i < S; ++i) {
+      tl[i] = tw + i * Dec::kStageBytes;
+      bk[i] = dec.block_of(min(t_first + i * st, t_last));
     }
-  } else if (my_n > 0) {
-    constexpr int L = Buf::kLoads;
-    Buf bA, bB;
-    // Block IDs run two steps ahead of the loads that use them.
-    uint32_t blk0 = dec.block_of(t_first);
-    uint32_t blk1 = dec.block_of(min(t_first + st, t_last));
-    uint32_t nextA = dec.block_of(min(t_first + 2 * st, t_last));
-    uint32_t nextB = dec.block_of(min(t_first + 3 * st, t_last));
-    scalar_ready(blk0);
-    scalar_ready(blk1);
-    if constexpr (kKLds) {
-      dec.issue_k_dma(tA, blk0, t_first);
-      dec.issue_v_dma(tA + Dec::kVOff, blk0, t_first);
-      dec.issue_k_dma(tB, blk1, min(t_first + st, t_last));
-      dec.issue_v_dma(tB + Dec::kVOff, blk1, min(t_first + st, t_last));
-    } else {
-      dec.issue(bA, tA, blk0, t_first);
-      if (!kFp8) dec.issue_v_dma(tA, blk0, t_first);
-      dec.issue(bB, tB, blk1, min(t_first + st, t_last));
-      if (!kFp8) dec.issue_v_dma(tB, blk1, min(t_first + st, t_last));
-    }
-    issue_q();
-    vm_wait_q<0>(qw, bA);
+#pragma unroll
+    for (int i = 0; i < S; ++i) nx[i] = dec.block_of(min(t_first + (S + i) * st, t_last));
+#pragma unroll
+    for (int i = 0; i < S; ++i) scalar_ready(bk[i]);
+#pragma unroll
+    for (int i = 0; i < S; ++i) dec.issue(tl[i], bk[i], min(t_first + i * st, t_last));
+    // Q is loaded after the first steps' K/V and waited for together with
+    // them, so a wave's start costs one memory round trip, not two.
     {
+      const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
+                             (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + min(dec.c, a.group - 1U)) *
+                                 kDim;
+      u32x4 qw[4];
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
+        vm_load16(qw[kc], qrow + dim);
+      }
+      vm_wait_all(qw);
       const bool live = dec.c < a.group;
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
     }
-    auto step = [&](Buf& b, uint8_t* tile, uint32_t& next, uint32_t t0) {
-      const uint32_t t2 = min(t0 + 2 * st, t_last);
-      vm_wait<L>(b);  // this step's loads; the next step's L stay in flight
-      scalar_ready(next);
-      if constexpr (kKLds) {
-        uint8_t* vtile = tile + Dec::kVOff;
-        dec.zero_dead_rows(vtile, t0);
-        wave_fence_lds();
-        const f32x4 s = dec.qk_lds(tile);
-        dec.softmax_pv(s, t0, vtile);
-        wait_lds_reads();
-        dec.issue_k_dma(tile, next, t2);
-        dec.issue_v_dma(vtile, next, t2);
-        wave_fence_lds();
-        next = dec.block_of(min(t0 + 4 * st, t_last));
-      } else {
-      if constexpr (kFp8) {
-        dec.stage_v_fp8(b, tile, t0);
-        wave_fence_lds();
-        const uint64_t vb = dec.row_base(dec.vbase, dec.vstride_b, dec.vstride_p, next, t2);
-        vm_load16_sv<0>(b.v[0], dec.v_voff, vb);
-        vm_load16_sv<16>(b.v[1], dec.v_voff, vb);
-      } else {
-        dec.zero_dead_rows(tile, t0);
-        wave_fence_lds();
-      }
-      const f32x4 s = dec.qk(b);
-      {
-        const uint64_t kb = dec.row_base(dec.kbase, dec.kstride_b, dec.kstride_p, next, t2);
-        vm_load16_sv<0>(b.k[0], dec.k_voff, kb);
-        vm_load16_sv<64>(b.k[1], dec.k_voff, kb);
-        if (!kFp8) {
-          vm_load16_sv<128>(b.k[2], dec.k_voff, kb);
-          vm_load16_sv<192>(b.k[3], dec.k_voff, kb);
+    for (uint32_t n = 0; n < my_n; n += S) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        if (n + i < my_n) {
+          const uint32_t t0 = t_first + (n + i) * st;
+          const uint32_t tn = min(t0 + S * st, t_last);
+          uint8_t* vtile = tl[i] + Dec::kVOff;
+          vm_wait_dma<Dec::kDmaPerStep * (S - 1)>();  // this step's loads; S - 1 steps stay in flight
+          scalar_ready(nx[i]);
+          if (kFp8) {
+            dec.stage_v_fp8(tl[i], t0);
+          } else {
+            dec.zero_dead_rows(vtile, t0);
+          }
+          wave_fence_lds();
+          const f32x4 sc = dec.qk(tl[i]);
+          dec.softmax_pv(sc, t0, vtile);
+          wait_lds_reads();
+          dec.issue(tl[i], nx[i], tn);
+          wave_fence_lds();
+          nx[i] = dec.block_of(min(t0 + 2 * S * st, t_last));
         }
       }
-      dec.softmax_pv(s, t0, tile);
-      if (!kFp8) {
-        wait_lds_reads();
-        dec.issue_v_dma(tile, next, t2);
-      }
-      wave_fence_lds();
-      next = dec.block_of(min(t0 + 4 * st, t_last));
-      }
-    };
-    for (uint32_t n = 0; n < my_n; n += 2) {
-      const uint32_t t0 = t_first + n * st;
-      step(bA, tA, nextA, t0);
-      if (n + 1 >= my_n) break;
-      step(bB, tB, nextB, t0 + st);
     }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   }
@@ -1922,9 +1769,7 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
 template <typename QE, bool kFp8, int kSplit>
 int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  // 16-bit caches take the all-LDS variant (whole-row loads for K as for V).
-  constexpr bool kKLds = !kFp8;
-  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit, kKLds>), dim3(static_cast<uint32_t>(grid)),
+  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kSplit * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
