@@ -872,6 +872,14 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
 constexpr uint32_t kStep = 16;
 constexpr uint32_t kStepTileBytes = kStep * kTileRowBytes;  // 4 KiB
 
+// Byte offset of 16-byte chunk ch of row t in a 16-bit V tile (256-byte
+// rows): chunk ch sits at ch ^ 2 (t & 7). The transposed reads fetch 8 bytes
+// per lane from rows 4g .. 4g + 3 for two lane groups g at a time; XORing
+// with three row bits spreads those eight rows over all 64 banks.
+__device__ __forceinline__ uint32_t vtile_off(uint32_t t, uint32_t ch) {
+  return t * kTileRowBytes + ((ch ^ ((t & 7U) << 1)) << 4);
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait_dma() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
@@ -912,8 +920,8 @@ struct StreamDecoder {
   uint64_t kbase, vbase;  // byte address of (block 0, page 0, this kv head)
   uint64_t kstride_b, vstride_b, kstride_p, vstride_p;  // byte strides
   uint32_t k_voff[4];  // 16-bit: lane's K DMA offset for rows 4i..4i+3
-  uint32_t v_voff;     // 16-bit: lane's V DMA offset within a 4-row group
-  uint32_t f8_k_voff, f8_v_voff;  // FP8: lane's K / V DMA offsets within 8 rows
+  uint32_t v_voff[2];  // 16-bit: lane's V DMA offset for even / odd 4-row groups
+  uint32_t f8_k_voff[2], f8_v_voff[2];  // FP8: lane's K / V DMA offsets, rows 8i .. 8i + 7
   float sl2;
 
   vec8 qb[4];
@@ -941,20 +949,26 @@ struct StreamDecoder {
   // Lane DMA offsets. 16-bit K: instruction i brings rows 4i + lane / 16;
   // row r keeps its 16-byte chunk L at position L ^ (r & 15), so the 16 rows
   // of one MFMA operand fetch fall in different bank groups. 16-bit V: chunk
-  // L of row r at L ^ 2 (r & 3), which the transposed reads need. FP8: eight
-  // 128-byte rows per instruction, chunk L of row r at L ^ (r & 7).
+  // L of row r at L ^ 2 (r & 7) (vtile_off). FP8: eight 128-byte rows per
+  // instruction, chunk L of row r at L ^ ((r >> 1) & 7), which keeps the K
+  // operand reads and the V conversion reads bank-conflict free.
   __device__ __forceinline__ void init_offsets() {
     if (kFp8) {
       const uint32_t row = lane >> 3;
-      const uint32_t chunk = ((lane & 7U) ^ (row & 7U)) << 4;
-      f8_k_voff = static_cast<uint32_t>(row * kstride_p) + chunk;
-      f8_v_voff = static_cast<uint32_t>(row * vstride_p) + chunk;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t chunk = ((lane & 7U) ^ (((8 * i + row) >> 1) & 7U)) << 4;
+        f8_k_voff[i] = static_cast<uint32_t>(row * kstride_p) + chunk;
+        f8_v_voff[i] = static_cast<uint32_t>(row * vstride_p) + chunk;
+      }
     } else {
       const uint32_t row = lane >> 4;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         k_voff[i] = static_cast<uint32_t>(row * kstride_p) + (((lane & 15U) ^ (4 * i + row)) << 4);
-      v_voff = static_cast<uint32_t>(row * vstride_p) + (((lane & 15U) ^ ((row & 3U) << 1)) << 4);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        v_voff[i] = static_cast<uint32_t>(row * vstride_p) + (((lane & 15U) ^ (((4 * i + row) & 7U) << 1)) << 4);
     }
   }
 
@@ -964,23 +978,26 @@ struct StreamDecoder {
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
     if (kFp8) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff, kb + 8 * i * kstride_p, stage + i * 1024);
+      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_v_voff, vb + 8 * i * vstride_p, stage + kF8TileBytes + i * 1024);
+      for (int i = 0; i < 2; ++i)
+        vm_load16_lds_sv(f8_v_voff[i], vb + 8 * i * vstride_p, stage + kF8TileBytes + i * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) vm_load16_lds_sv(k_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(v_voff, vb + 4 * i * vstride_p, stage + kVOff + i * 1024);
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(v_voff[i & 1], vb + 4 * i * vstride_p, stage + kVOff + i * 1024);
     }
   }
 
   // MFMA A operand kc of token c. 16-bit: dims kc*32 + g*8 .. +7. FP8: dims
-  // (kc >> 1)*64 + g*16 + (kc & 1)*8 .. +7, converted (Q uses the same dims).
+  // (kc >> 1)*64 + g*16 + ((kc ^ g) & 1)*8 .. +7, converted (Q uses the same
+  // dims); the half depends on g so that the two lane groups served together
+  // read different banks.
   __device__ __forceinline__ vec8 k_operand(const uint8_t* stage, int kc) const {
     if (kFp8) {
-      const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ (c & 7U);
-      const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kDim + chunk * 16 + (kc & 1) * 8);
+      const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ ((c >> 1) & 7U);
+      const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kDim + chunk * 16 + ((kc ^ g) & 1U) * 8);
       return Ops::from_fp8(w.x, w.y);
     } else {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ c;
@@ -1005,14 +1022,18 @@ struct StreamDecoder {
     const bool live = t0 + t < len;
     const uint8_t* vrow = stage + kF8TileBytes + t * kDim;
     uint8_t* tile = stage + kVOff;
+    const uint32_t odd = lane & 1U;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t lc = (lane & 3U) * 2 + h;  // logical 16-byte chunk of the FP8 row
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ (t & 7U)) << 4));
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ ((t >> 1) & 7U)) << 4));
       const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
-      const uint32_t ch = lc * 2;  // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each)
-      *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = Ops::from_fp8(w[0], w[1]);
-      *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = Ops::from_fp8(w[2], w[3]);
+      // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each); odd lanes store the
+      // upper one first so that each store instruction spans all banks.
+      const vec8 lo = Ops::from_fp8(w[0], w[1]), hi = Ops::from_fp8(w[2], w[3]);
+      const uint32_t ch = lc * 2;
+      *reinterpret_cast<vec8*>(tile + vtile_off(t, ch + odd)) = odd ? hi : lo;
+      *reinterpret_cast<vec8*>(tile + vtile_off(t, ch + 1 - odd)) = odd ? lo : hi;
     }
   }
 
@@ -1060,7 +1081,7 @@ struct StreamDecoder {
     lds_u8* base = (lds_u8*)tile;
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; ++dt) {
-      const uint32_t off = tile_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
+      const uint32_t off = vtile_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
       const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
       acc[dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb, acc[dt]);
     }
@@ -1235,7 +1256,7 @@ void decode_stream_kernel(DecodeArgs a) {
       u32x4 qw[4];
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + (kc & 1) * 8) : (kc * 32 + dec.g * 8);
+        const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
         vm_load16(qw[kc], qrow + dim);
       }
       vm_wait_all(qw);
