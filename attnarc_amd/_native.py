@@ -26,6 +26,7 @@ KV_CACHE_NATIVE = 0
 KV_CACHE_FP8_E4M3 = 1
 
 F32, F16, BF16 = 0, 1, 2
+ROPE_PAGED_KV_WRITE = 5
 PAGED_DECODE_ATTENTION = 9
 KERNEL_DECODE, KERNEL_MERGE = 0, 1
 
@@ -38,6 +39,7 @@ F = ctypes.c_float
 _BASE = [P, P, P, P, P, P] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _SPLIT = [P, P, P, P, P, P, P, U64] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _EXT = [P, P, P, P, P, P, P, P, P, P, U64] + [U32] * 9 + [U64] * 6 + [U32, U32, U32, F, P]
+_ROPE = [P] * 10 + [U32] * 12 + [U64] * 12 + [U32, P]
 SIGNATURES = {
     "loom_hip_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "loom_hip_paged_decode_attention_f32": (_BASE, ctypes.c_int),
@@ -55,6 +57,9 @@ SIGNATURES = {
         [U32] * 11 + [F, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p)],
         ctypes.c_int,
     ),
+    "loom_hip_rope_paged_kv_write_f32": (_ROPE, ctypes.c_int),
+    "loom_hip_rope_paged_kv_write_f16": (_ROPE, ctypes.c_int),
+    "loom_hip_rope_paged_kv_write_bf16": (_ROPE, ctypes.c_int),
     "loom_hip_backend_name": ([], ctypes.c_char_p),
     "loom_hip_abi_version": ([], U32),
     "loom_hip_last_error_message": ([], ctypes.c_char_p),

@@ -1,8 +1,8 @@
 """Build recipe of the in-tree HIP library ``_build/libloom_hip.so`` (gfx950).
 
-hipcc compiles the kernels and the C ABI in one translation unit. Packed FP32
-instruction selection is disabled (``-packed-fp32-ops``) for every HIP
-translation unit built here.
+hipcc compiles the paged-decode kernels with the C ABI and the RoPE + paged
+K/V write kernel into one shared library. Packed FP32 instruction selection is
+disabled (``-packed-fp32-ops``) for every HIP translation unit built here.
 """
 
 from __future__ import annotations
@@ -12,7 +12,10 @@ import subprocess
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
-SOURCE = os.path.join(PKG_DIR, "csrc", "paged_decode_attention.hip")
+SOURCES = [
+    os.path.join(PKG_DIR, "csrc", "paged_decode_attention.hip"),
+    os.path.join(PKG_DIR, "csrc", "rope_paged_kv.hip"),
+]
 LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip.so")
 PROBE_SOURCE = os.path.join(PKG_DIR, "csrc", "hbm_probe.hip")
 PROBE_LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip_probe.so")
@@ -30,10 +33,10 @@ HIPCC_FLAGS = [
 ]
 
 
-def _compile(source: str, out: str, verbose: bool) -> None:
+def _compile(sources, out: str, verbose: bool) -> None:
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [HIPCC, *HIPCC_FLAGS, source, "-o", tmp]
+    cmd = [HIPCC, *HIPCC_FLAGS, *sources, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
@@ -42,8 +45,8 @@ def _compile(source: str, out: str, verbose: bool) -> None:
 
 def build(verbose: bool = False) -> str:
     """Compile the decode library and the HBM probe library; returns the former's path."""
-    _compile(SOURCE, LIB_PATH, verbose)
-    _compile(PROBE_SOURCE, PROBE_LIB_PATH, verbose)
+    _compile(SOURCES, LIB_PATH, verbose)
+    _compile([PROBE_SOURCE], PROBE_LIB_PATH, verbose)
     return LIB_PATH
 
 

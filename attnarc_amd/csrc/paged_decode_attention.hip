@@ -41,6 +41,7 @@
 #include <vector>
 
 #include "../../include/loom_hip.h"
+#include "loom_hip_internal.h"
 
 namespace {
 
@@ -1530,6 +1531,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
 // ---------------------------------------------------------------------------
 thread_local std::string g_last_error;
 std::atomic<uint64_t> g_decode_launches{0};
+std::atomic<uint64_t> g_rope_launches{0};
 
 int fail(int status, const char* message) {
   g_last_error = message;
@@ -2068,6 +2070,19 @@ Problem extended_problem(uint32_t dtype, const void* query, const void* key_cach
 
 }  // namespace
 
+namespace loom_hip_detail {
+
+int fail(int status, const char* message) { return ::fail(status, message); }
+
+int device_available() { return ::device_available(); }
+
+void count_launch(uint32_t operation) {
+  if (operation == LOOM_HIP_PAGED_DECODE_ATTENTION) g_decode_launches.fetch_add(1, std::memory_order_relaxed);
+  if (operation == LOOM_HIP_ROPE_PAGED_KV_WRITE) g_rope_launches.fetch_add(1, std::memory_order_relaxed);
+}
+
+}  // namespace loom_hip_detail
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -2091,13 +2106,19 @@ uint32_t loom_hip_abi_version(void) { return 1; }
 const char* loom_hip_last_error_message(void) { return g_last_error.c_str(); }
 
 int loom_hip_launch_count(uint32_t operation, uint64_t* count) {
-  if (operation != LOOM_HIP_PAGED_DECODE_ATTENTION || count == nullptr)
+  if ((operation != LOOM_HIP_PAGED_DECODE_ATTENTION && operation != LOOM_HIP_ROPE_PAGED_KV_WRITE) ||
+      count == nullptr)
     return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown operator id or null count");
-  *count = g_decode_launches.load(std::memory_order_relaxed);
+  *count = (operation == LOOM_HIP_PAGED_DECODE_ATTENTION ? g_decode_launches : g_rope_launches)
+               .load(std::memory_order_relaxed);
   return LOOM_HIP_SUCCESS;
 }
 
 int loom_hip_reset_launch_count(uint32_t operation) {
+  if (operation == LOOM_HIP_ROPE_PAGED_KV_WRITE) {
+    g_rope_launches.store(0, std::memory_order_relaxed);
+    return LOOM_HIP_SUCCESS;
+  }
   if (operation != LOOM_HIP_PAGED_DECODE_ATTENTION)
     return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown operator id");
   g_decode_launches.store(0, std::memory_order_relaxed);

@@ -434,6 +434,219 @@ def paged_decode_attention_extended(
 
 
 # ---------------------------------------------------------------------------
+# Fused RoPE + paged K/V cache write.
+# ---------------------------------------------------------------------------
+
+
+def supports_rope_paged_kv_write(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    kv_cache: torch.Tensor,
+    key_scales: torch.Tensor,
+    value_scales: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> bool:
+    """Whether the tensors match the native/FP8 RoPE+paged-write ABI.
+
+    Same predicate as python/src/loom_kernels/ops/rope_kv.py:11-97.
+    """
+    try:
+        _check_rope_paged_kv_write_contract(
+            query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping
+        )
+    except RuntimeError:
+        return False
+    return not any(t.requires_grad for t in (query, key, value, cos_sin_cache))
+
+
+def _kv_span(kv_cache: torch.Tensor, dims: tuple[int, ...]) -> int:
+    return 1 + sum((kv_cache.shape[d] - 1) * kv_cache.stride(d) for d in dims)
+
+
+def _check_rope_paged_kv_write_contract(
+    query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping,
+) -> None:
+    """python/csrc/rope_kv.cpp:37-133 and the ABI limits of :141-150."""
+    def check(cond, msg):
+        if not cond:
+            raise RuntimeError(msg)
+
+    check(query.is_cuda, "Loom RoPE+paged-KV query must be on a GPU")
+    check(
+        all(t.device == query.device for t in (
+            key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping)),
+        "Loom RoPE+paged-KV tensors must be on one GPU device",
+    )
+    check(
+        key.dtype == query.dtype and value.dtype == query.dtype and cos_sin_cache.dtype == query.dtype,
+        "Loom RoPE+paged-KV Q/K/V and cos/sin cache must share a dtype",
+    )
+    check(query.dtype in _DTYPE_CODES, "Loom RoPE+paged-KV supports F32, FP16, and BF16 sources")
+    check(query.dim() == 3 and key.dim() == 3 and value.dim() == 3, "Loom RoPE+paged-KV Q/K/V must have rank 3")
+    check(
+        kv_cache.dtype == query.dtype or kv_cache.dtype == torch.uint8,
+        "Loom paged K/V cache must use the source dtype or uint8 FP8 E4M3 storage",
+    )
+    check(
+        key_scales.dtype == torch.float32 and value_scales.dtype == torch.float32
+        and key_scales.is_contiguous() and value_scales.is_contiguous()
+        and key_scales.numel() == value_scales.numel()
+        and key_scales.numel() in (1, key.shape[1]),
+        "Loom paged K/V cache scales must be contiguous float32 tensors with one element or one element per KV head",
+    )
+    check(
+        positions.dtype == torch.int64 and slot_mapping.dtype == torch.int64,
+        "Loom RoPE+paged-KV positions and slot mapping must be int64",
+    )
+    check(min(query.shape) > 0, "Loom RoPE+paged-KV query must be non-empty")
+    check(
+        key.shape[0] == query.shape[0] and value.shape[0] == query.shape[0],
+        "Loom RoPE+paged-KV Q/K/V token counts must match",
+    )
+    check(key.shape[1] > 0 and key.shape[1] == value.shape[1], "Loom RoPE+paged-KV K/V head counts must match")
+    check(key.shape[2] == query.shape[2], "Loom RoPE+paged-KV Q/K head sizes must match")
+    check(value.shape[2] > 0, "Loom RoPE+paged-KV value head size must be positive")
+    check(
+        query.stride(2) == 1 and key.stride(2) == 1 and value.stride(2) == 1
+        and min(query.stride(0), query.stride(1), key.stride(0), key.stride(1),
+                value.stride(0), value.stride(1)) > 0
+        and positions.is_contiguous() and cos_sin_cache.is_contiguous() and slot_mapping.is_contiguous(),
+        "Loom RoPE+paged-KV sources require unit dim stride and positive token/head strides; "
+        "metadata must be contiguous",
+    )
+    check(
+        positions.dim() == 1 and positions.numel() == query.shape[0]
+        and slot_mapping.dim() == 1 and slot_mapping.numel() <= query.shape[0],
+        "Loom RoPE positions must cover every token and slot_mapping must not exceed the padded token count",
+    )
+    check(
+        cos_sin_cache.dim() == 2 and cos_sin_cache.shape[0] > 0 and cos_sin_cache.shape[1] > 0
+        and cos_sin_cache.shape[1] % 2 == 0 and cos_sin_cache.shape[1] <= query.shape[2],
+        "Loom RoPE+paged-KV cos/sin cache must be [max_position, even rotary_dim <= head_size]",
+    )
+    check(
+        kv_cache.dim() == 5 and kv_cache.shape[1] == 2,
+        "Loom paged K/V cache must have shape [blocks, 2, block_size, kv_heads, head_size]",
+    )
+    check(
+        kv_cache.shape[0] > 0 and kv_cache.shape[2] > 0 and kv_cache.shape[3] == key.shape[1]
+        and kv_cache.shape[4] == key.shape[2] and value.shape[1] == key.shape[1]
+        and value.shape[2] == key.shape[2],
+        "Loom packed K/V cache and K/V sources must share head count and head size",
+    )
+    check(
+        kv_cache.stride(4) == 1 and min(kv_cache.stride()[:4]) > 0,
+        "Loom packed K/V cache requires unit element stride and positive block/KV/page/head strides",
+    )
+    part = _kv_span(kv_cache, (2, 3, 4))
+    check(
+        kv_cache.stride(1) >= part and kv_cache.stride(0) >= kv_cache.stride(1)
+        and kv_cache.stride(0) - kv_cache.stride(1) >= part,
+        "Loom packed K/V cache partitions must not overlap",
+    )
+    check(
+        _u32(query.shape[0], query.shape[1], key.shape[1], query.shape[2], value.shape[2],
+             cos_sin_cache.shape[1], cos_sin_cache.shape[0], kv_cache.shape[0], kv_cache.shape[2])
+        and query.shape[0] <= 0x7FFF_FFFF,
+        "Loom RoPE+paged-KV shape exceeds the HIP ABI",
+    )
+
+
+def rope_paged_kv_write_(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    kv_cache: torch.Tensor,
+    key_scales: torch.Tensor,
+    value_scales: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    is_neox: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Rotate Q/K in place and write native or scaled FP8 E4M3 paged K/V caches.
+
+    Mirrors python/src/loom_kernels/ops/rope_kv.py:100-134 and the adapter
+    python/csrc/rope_kv.cpp:135-220. ``kv_cache`` is
+    [blocks, 2, block_size, kv_heads, head_size] (K at index 0, V at 1) in the
+    source dtype, or uint8 holding FP8 E4M3FN bytes. Scale tensors are always
+    passed; native caches ignore them, FP8 caches index them per tensor (one
+    element) or per KV head. ``slot_mapping`` covers the first
+    ``slot_mapping.numel()`` tokens; negative slots are padding. Returns
+    ``(query, key, kv_cache)``.
+    """
+    _require_inference_tensors(query, key, value, cos_sin_cache, kv_cache, key_scales, value_scales)
+    _check_rope_paged_kv_write_contract(
+        query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping
+    )
+    value_cache = kv_cache[:, 1]
+    block, page, head = kv_cache.stride(0), kv_cache.stride(2), kv_cache.stride(3)
+    rope_paged_kv_write_strided(
+        query, key, value, positions, cos_sin_cache, kv_cache[:, 0], value_cache,
+        key_scales, value_scales, slot_mapping,
+        num_blocks=int(kv_cache.shape[0]), block_size=int(kv_cache.shape[2]),
+        key_cache_strides=(block, page, head), value_cache_strides=(block, page, head),
+        scale_stride=0 if key_scales.numel() == 1 else 1, is_neox=is_neox,
+    )
+    return query, key, kv_cache
+
+
+def rope_paged_kv_write_strided(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    key_scales: torch.Tensor | None,
+    value_scales: torch.Tensor | None,
+    slot_mapping: torch.Tensor | None,
+    *,
+    num_blocks: int,
+    block_size: int,
+    key_cache_strides: tuple[int, int, int],
+    value_cache_strides: tuple[int, int, int],
+    scale_stride: int = 0,
+    is_neox: bool = True,
+) -> None:
+    """Direct binding of ``loom_hip_rope_paged_kv_write_*`` over explicit strides.
+
+    Caches are separate K and V tensors addressed through (block, page, head)
+    element strides, so NHD ([blocks, block_size, heads, dim]), HND
+    ([blocks, heads, block_size, dim]) and packed views all fit. A uint8 (or
+    float8_e4m3fn) key cache selects FP8 E4M3 encoding with the given scales.
+    Native caches ignore the scales (they may be None). The caller is
+    responsible for the storage covering every addressed slot.
+    """
+    if query.dtype not in _DTYPE_CODES:
+        raise RuntimeError("Loom RoPE+paged-KV supports F32, FP16, and BF16 sources")
+    fp8 = key_cache.dtype in _FP8_DTYPES
+    encoding = _native.KV_CACHE_FP8_E4M3 if fp8 else _native.KV_CACHE_NATIVE
+    if fp8 and (key_scales is None or value_scales is None):
+        raise RuntimeError("Loom RoPE+paged-KV FP8 caches require key and value scales")
+    tokens = int(query.shape[0])
+    cache_tokens = 0 if slot_mapping is None else int(slot_mapping.numel())
+    code = _DTYPE_CODES[query.dtype]
+    suffix = {_native.F32: "f32", _native.F16: "f16", _native.BF16: "bf16"}[code]
+    with torch.cuda.device(query.device):
+        status = getattr(_native.lib(), f"loom_hip_rope_paged_kv_write_{suffix}")(
+            _ptr(query), _ptr(key), _ptr(value), _ptr(positions), _ptr(cos_sin_cache),
+            _ptr(key_cache), _ptr(value_cache), _ptr(key_scales), _ptr(value_scales),
+            _ptr(slot_mapping) if cache_tokens else None,
+            tokens, cache_tokens, int(query.shape[1]), int(key.shape[1]), int(query.shape[2]),
+            int(value.shape[2]), int(cos_sin_cache.shape[1]), int(cos_sin_cache.shape[0]),
+            int(num_blocks), int(block_size), encoding, int(scale_stride),
+            query.stride(0), query.stride(1), key.stride(0), key.stride(1), value.stride(0), value.stride(1),
+            *key_cache_strides, *value_cache_strides, 1 if is_neox else 0, _stream_handle(query.device),
+        )
+    _native.check(status, "Loom RoPE+paged-KV")
+
+
+# ---------------------------------------------------------------------------
 # Capability query and telemetry.
 # ---------------------------------------------------------------------------
 

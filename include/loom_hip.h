@@ -59,6 +59,7 @@ enum LoomHipDType {
 
 /* Operator ids for launch telemetry: loom_cuda_bridge.h:28-40. */
 enum LoomHipOperator {
+  LOOM_HIP_ROPE_PAGED_KV_WRITE = 5,
   LOOM_HIP_PAGED_DECODE_ATTENTION = 9,
 };
 
@@ -247,6 +248,70 @@ int loom_hip_paged_decode_attention_supports(
     uint32_t value_head_size, uint32_t num_blocks, uint32_t block_size,
     uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
     float scale, const char** reason, const char** kernel_family);
+
+/*
+ * Fused rotary embedding + paged K/V cache write. Replaces
+ * loom_cuda_rope_paged_kv_write_{f32,f16,bf16} (loom_cuda.h:252-318) with the
+ * same argument list and meaning (contract: crates/loom-kernels/src/
+ * rope_kv.rs:513-631). Q [tokens, query_heads, head_size] and K
+ * [tokens, kv_heads, head_size] are rotated in place over the first
+ * rotary_dim dims (is_neox 1: pairs (p, p + rotary_dim/2); 0: (2p, 2p+1))
+ * with cos/sin from cos_sin_cache[position, 0:rotary_dim/2 | rotary_dim/2:].
+ * For token < cache_tokens with 0 <= slot_mapping[token] < num_blocks *
+ * block_size, the rotated K row and the V row [value_head_size] are stored at
+ * block = slot / block_size, page = slot % block_size through the cache
+ * block/page/head element strides. cache_encoding FP8_E4M3 stores
+ * e4m3fn(x / scale[kv_head * scale_stride]) (round to nearest even, finite
+ * saturation); native stores the element type. Tokens with a position
+ * outside [0, max_position) are not touched. All strides are in elements.
+ */
+int loom_hip_rope_paged_kv_write_f32(
+    float* query, float* key, const float* value, const int64_t* positions,
+    const float* cos_sin_cache, void* key_cache, void* value_cache,
+    const float* key_scales, const float* value_scales,
+    const int64_t* slot_mapping, uint32_t tokens, uint32_t cache_tokens,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t rotary_dim, uint32_t max_position,
+    uint32_t num_blocks, uint32_t block_size, uint32_t cache_encoding,
+    uint32_t scale_stride, uint64_t query_token_stride,
+    uint64_t query_head_stride, uint64_t key_token_stride,
+    uint64_t key_head_stride, uint64_t value_token_stride,
+    uint64_t value_head_stride, uint64_t key_cache_block_stride,
+    uint64_t key_cache_page_stride, uint64_t key_cache_head_stride,
+    uint64_t value_cache_block_stride, uint64_t value_cache_page_stride,
+    uint64_t value_cache_head_stride, uint32_t is_neox, void* stream);
+
+int loom_hip_rope_paged_kv_write_f16(
+    uint16_t* query, uint16_t* key, const uint16_t* value,
+    const int64_t* positions, const uint16_t* cos_sin_cache, void* key_cache,
+    void* value_cache, const float* key_scales, const float* value_scales,
+    const int64_t* slot_mapping, uint32_t tokens, uint32_t cache_tokens,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t rotary_dim, uint32_t max_position,
+    uint32_t num_blocks, uint32_t block_size, uint32_t cache_encoding,
+    uint32_t scale_stride, uint64_t query_token_stride,
+    uint64_t query_head_stride, uint64_t key_token_stride,
+    uint64_t key_head_stride, uint64_t value_token_stride,
+    uint64_t value_head_stride, uint64_t key_cache_block_stride,
+    uint64_t key_cache_page_stride, uint64_t key_cache_head_stride,
+    uint64_t value_cache_block_stride, uint64_t value_cache_page_stride,
+    uint64_t value_cache_head_stride, uint32_t is_neox, void* stream);
+
+int loom_hip_rope_paged_kv_write_bf16(
+    uint16_t* query, uint16_t* key, const uint16_t* value,
+    const int64_t* positions, const uint16_t* cos_sin_cache, void* key_cache,
+    void* value_cache, const float* key_scales, const float* value_scales,
+    const int64_t* slot_mapping, uint32_t tokens, uint32_t cache_tokens,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size,
+    uint32_t value_head_size, uint32_t rotary_dim, uint32_t max_position,
+    uint32_t num_blocks, uint32_t block_size, uint32_t cache_encoding,
+    uint32_t scale_stride, uint64_t query_token_stride,
+    uint64_t query_head_stride, uint64_t key_token_stride,
+    uint64_t key_head_stride, uint64_t value_token_stride,
+    uint64_t value_head_stride, uint64_t key_cache_block_stride,
+    uint64_t key_cache_page_stride, uint64_t key_cache_head_stride,
+    uint64_t value_cache_block_stride, uint64_t value_cache_page_stride,
+    uint64_t value_cache_head_stride, uint32_t is_neox, void* stream);
 
 /* Backend name, as CudaBackend::name() = "loom-cuda" (cuda_backend.rs:43). */
 const char* loom_hip_backend_name(void);

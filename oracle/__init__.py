@@ -4,9 +4,10 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package. It is the checker the HIP path is
 compared against and is never called by the product library.
 
-The C++ restatement lives in ``paged_decode_oracle.cpp``; each function there
-cites the Rust reference (``crates/loom-kernels/src/attention.rs`` and
-friends) it follows. Arrays are numpy: F32 as ``float32``, F16 as
+The C++ restatements live in ``paged_decode_oracle.cpp`` (paged decode) and
+``rope_kv_oracle.cpp`` (RoPE + paged K/V write); each function there cites
+the Rust reference (``crates/loom-kernels/src/attention.rs``, ``rope_kv.rs``
+and friends) it follows. Arrays are numpy: F32 as ``float32``, F16 as
 ``float16``, BF16 as raw ``uint16`` bit patterns, FP8 E4M3FN as ``uint8``.
 """
 
@@ -35,6 +36,13 @@ MAX_SEQUENCE_LENGTH_OUT_OF_BOUNDS = 6
 BLOCK_ID_OUT_OF_BOUNDS = 7
 LENGTH_MISMATCH = 8
 UNSUPPORTED_DTYPE = 9
+INVALID_ROTARY_DIMENSION = 10
+POSITION_OUT_OF_BOUNDS = 11
+SLOT_OUT_OF_BOUNDS = 12
+DUPLICATE_SLOT = 13
+
+NEOX, INTERLEAVED = 0, 1
+PER_TENSOR, PER_HEAD = 0, 1
 
 
 class OracleSpec(ctypes.Structure):
@@ -63,6 +71,30 @@ class OracleError(ctypes.Structure):
         ("fvalue", ctypes.c_float),
         ("buffer", ctypes.c_char * 32),
         ("message", ctypes.c_char * 256),
+    ]
+
+
+class OracleRotarySpec(ctypes.Structure):
+    _fields_ = [
+        ("tokens", ctypes.c_uint64),
+        ("query_heads", ctypes.c_uint64),
+        ("key_heads", ctypes.c_uint64),
+        ("head_size", ctypes.c_uint64),
+        ("rotary_dim", ctypes.c_uint64),
+        ("max_position", ctypes.c_uint64),
+        ("dtype", ctypes.c_int32),
+        ("style", ctypes.c_int32),
+    ]
+
+
+class OracleRopeWriteSpec(ctypes.Structure):
+    _fields_ = [
+        ("rotary", OracleRotarySpec),
+        ("value_head_size", ctypes.c_uint64),
+        ("num_blocks", ctypes.c_uint64),
+        ("block_size", ctypes.c_uint64),
+        ("encoding", ctypes.c_int32),
+        ("granularity", ctypes.c_int32),
     ]
 
 
@@ -139,6 +171,21 @@ def lib() -> ctypes.CDLL:
         for name in ("oracle_fp8_encode_array", "oracle_bf16_encode_array", "oracle_f16_encode_array"):
             getattr(l, name).argtypes = [P, P, U64]
             getattr(l, name).restype = None
+        I32 = ctypes.c_int32
+        l.oracle_rotary_spec_new.argtypes = [U64] * 6 + [I32, I32, ctypes.POINTER(OracleRotarySpec),
+                                                          ctypes.POINTER(OracleError)]
+        l.oracle_rotary_spec_new.restype = I32
+        l.oracle_rope_write_spec_new.argtypes = [ctypes.POINTER(OracleRotarySpec), U64, U64, U64, I32, I32,
+                                                 ctypes.POINTER(OracleRopeWriteSpec), ctypes.POINTER(OracleError)]
+        l.oracle_rope_write_spec_new.restype = I32
+        l.oracle_rope_scale_elements.argtypes = [ctypes.POINTER(OracleRopeWriteSpec)]
+        l.oracle_rope_scale_elements.restype = U64
+        l.oracle_rotary_embedding.argtypes = [P, U64, P, U64, P, U64, P, U64, ctypes.POINTER(OracleRotarySpec), I32,
+                                              ctypes.POINTER(OracleError)]
+        l.oracle_rotary_embedding.restype = I32
+        l.oracle_rope_paged_kv_write.argtypes = [P, U64] * 10 + [ctypes.POINTER(OracleRopeWriteSpec), I32,
+                                                                 ctypes.POINTER(OracleError)]
+        l.oracle_rope_paged_kv_write.restype = I32
         _lib = l
     return _lib
 
@@ -316,3 +363,75 @@ def encode_f16(values: np.ndarray) -> np.ndarray:
 
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# RoPE + paged K/V write (rope_kv_oracle.cpp)
+# ---------------------------------------------------------------------------
+
+
+def rotary_spec_new(tokens, query_heads, key_heads, head_size, rotary_dim, max_position, dtype, style=NEOX):
+    """RotaryEmbeddingSpec::new (rope_kv.rs:66-113); raises ContractError."""
+    spec = OracleRotarySpec()
+    err = OracleError()
+    rc = lib().oracle_rotary_spec_new(tokens, query_heads, key_heads, head_size, rotary_dim, max_position, dtype,
+                                      style, ctypes.byref(spec), ctypes.byref(err))
+    if rc != 0:
+        _raise(err)
+    return spec
+
+
+def rope_write_spec_new(rotary, value_head_size, num_blocks, block_size, encoding=NATIVE, granularity=PER_TENSOR):
+    """RopePagedKvWriteSpec::new (rope_kv.rs:176-211); raises ContractError."""
+    spec = OracleRopeWriteSpec()
+    err = OracleError()
+    rc = lib().oracle_rope_write_spec_new(ctypes.byref(rotary), value_head_size, num_blocks, block_size, encoding,
+                                          granularity, ctypes.byref(spec), ctypes.byref(err))
+    if rc != 0:
+        _raise(err)
+    return spec
+
+
+def rope_scale_elements(spec) -> int:
+    """RopePagedKvWriteSpec::scale_elements (rope_kv.rs:232-234)."""
+    return int(lib().oracle_rope_scale_elements(ctypes.byref(spec)))
+
+
+def rotary_embedding(query, key, positions, cos_sin_cache, spec, dtype=None):
+    """rotary_embedding_*_reference (rope_kv.rs:499-511): rotates copies of
+    ``query`` and ``key`` and returns them; raises ContractError."""
+    q = np.ascontiguousarray(query).copy()
+    k = np.ascontiguousarray(key).copy()
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    cs = np.ascontiguousarray(cos_sin_cache)
+    err = OracleError()
+    rc = lib().oracle_rotary_embedding(_ptr(q), q.size, _ptr(k), k.size, _ptr(pos), pos.size, _ptr(cs), cs.size,
+                                       ctypes.byref(spec), spec.dtype if dtype is None else dtype, ctypes.byref(err))
+    if rc != 0:
+        _raise(err)
+    return q, k
+
+
+def rope_paged_kv_write(query, key, value, positions, cos_sin_cache, key_cache, value_cache, slot_mapping, spec,
+                        key_scales=None, value_scales=None, dtype=None):
+    """rope_paged_kv_write_*_reference and the FP8 variant (rope_kv.rs:513-631)
+    on contiguous NHD caches. Works on copies and returns (query, key,
+    key_cache, value_cache); raises ContractError (nothing changed)."""
+    q = np.ascontiguousarray(query).copy()
+    k = np.ascontiguousarray(key).copy()
+    v = np.ascontiguousarray(value)
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    cs = np.ascontiguousarray(cos_sin_cache)
+    kc = np.ascontiguousarray(key_cache).copy()
+    vc = np.ascontiguousarray(value_cache).copy()
+    slots = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    ks = np.ascontiguousarray(key_scales if key_scales is not None else np.zeros(0), dtype=np.float32)
+    vs = np.ascontiguousarray(value_scales if value_scales is not None else np.zeros(0), dtype=np.float32)
+    err = OracleError()
+    rc = lib().oracle_rope_paged_kv_write(
+        _ptr(q), q.size, _ptr(k), k.size, _ptr(v), v.size, _ptr(pos), pos.size, _ptr(cs), cs.size,
+        _ptr(kc), kc.size, _ptr(vc), vc.size, _ptr(slots), slots.size, _ptr(ks), ks.size, _ptr(vs), vs.size,
+        ctypes.byref(spec), spec.rotary.dtype if dtype is None else dtype, ctypes.byref(err))
+    if rc != 0:
+        _raise(err)
+    return q, k, kc, vc

@@ -33,6 +33,8 @@
 #include <limits>
 #include <vector>
 
+#include "oracle.h"
+
 namespace {
 
 enum DType : int32_t { kF32 = 0, kF16 = 1, kBf16 = 2, kFp8E4M3Fn = 3 };
@@ -63,34 +65,6 @@ const char* dtype_debug_name(int32_t dtype) {
 
 }  // namespace
 
-extern "C" {
-
-struct OracleSpec {
-  uint64_t sequences;
-  uint64_t query_heads;
-  uint64_t kv_heads;
-  uint64_t head_size;
-  uint64_t value_head_size;
-  uint64_t num_blocks;
-  uint64_t block_size;
-  uint64_t max_blocks_per_sequence;
-  uint64_t max_sequence_length;
-  float scale;
-  int32_t dtype;
-};
-
-struct OracleError {
-  int32_t kind;
-  uint64_t a;  // first usize field of the variant
-  uint64_t b;  // second usize field
-  uint64_t c;  // third usize field
-  int64_t value;  // i64 field (length / block_id)
-  float fvalue;   // f32 field (scale)
-  char buffer[32];
-  char message[256];
-};
-
-}  // extern "C"
 
 namespace {
 
