@@ -77,6 +77,37 @@ __device__ __forceinline__ uint8_t encode_e4m3fn(float x) {
   return sign | static_cast<uint8_t>(code > 0x7eU ? 0x7eU : code);
 }
 
+// Vector-path FP8 helpers. The packed hardware conversion rounds to nearest
+// even into OCP E4M3FN; saturation to +-448 is applied first (it returns NaN
+// on overflow otherwise) and NaN inputs are re-encoded in software, since the
+// hardware sets the sign bit of every NaN where the reference keeps it.
+__device__ __forceinline__ float sat448(float x) {
+  return __builtin_fabsf(x) > 448.0f ? __builtin_copysignf(448.0f, x) : x;
+}
+
+// Correctly rounded a / b given y = RN(1 / b): q = RN(a * y) is within one
+// ulp, r = a - q * b is exact by FMA, and RN(q + r * y) = RN(a / b)
+// (Markstein's theorem). Outside the range where no intermediate can
+// underflow or overflow the quotient falls back to IEEE division; that range
+// only holds quotients that encode to +-0 or saturate.
+__device__ __forceinline__ float div_rn(float a, float b, float y) {
+  const float q = a * y;
+  if (!(__builtin_fabsf(a) >= 0x1p-100f && __builtin_fabsf(q) <= 0x1p20f)) return a / b;
+  const float r = __builtin_fmaf(-q, b, a);
+  return __builtin_fmaf(r, y, q);
+}
+
+// Four values -> four E4M3FN bytes (little-endian in one dword).
+__device__ __forceinline__ uint32_t encode4_e4m3fn(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(sat448(a), sat448(b), 0, false);
+  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(sat448(c), sat448(d), lo, true));
+  if (__builtin_expect(__builtin_isnan(a) | __builtin_isnan(b) | __builtin_isnan(c) | __builtin_isnan(d), 0)) {
+    w = static_cast<uint32_t>(encode_e4m3fn(a)) | (static_cast<uint32_t>(encode_e4m3fn(b)) << 8) |
+        (static_cast<uint32_t>(encode_e4m3fn(c)) << 16) | (static_cast<uint32_t>(encode_e4m3fn(d)) << 24);
+  }
+  return w;
+}
+
 struct RopeArgs {
   void* query;
   void* key;
@@ -161,6 +192,180 @@ __global__ __launch_bounds__(kRopeThreads) void rope_paged_kv_kernel(RopeArgs a)
   for (uint32_t d = lane; d < a.value_head_size; d += 64) put(vdst, d, v[d], vscale);
 }
 
+// Vector path: one workgroup per (token, split); every thread moves whole
+// 16-byte chunks. Items of a token, in order:
+//   Q rotary items  query_heads * rot_items
+//   K rotary items  kv_heads * rot_items          (also stored to the K cache)
+//   K tail chunks   kv_heads * tail_chunks         (only when the token has a slot)
+//   V chunks        kv_heads * value_chunks        (only when the token has a slot)
+// A NeoX rotary item is chunk c of the first half plus chunk c of the second
+// half (pairs (p, p + rotary_dim/2) stay in-lane); an interleaved item is one
+// chunk holding VEC/2 adjacent pairs. Each thread takes kUnroll items and
+// issues all of their loads before any arithmetic, so a workgroup keeps
+// ~kUnroll * 256 * 48 bytes in flight.
+constexpr uint32_t kVecUnroll = 2;
+
+template <typename E>
+struct Vec {
+  using T = typename E::T;
+  static constexpr uint32_t N = 16 / sizeof(T);  // elements per 16-byte chunk
+  union Chunk {
+    uint4 raw;
+    T v[N];
+  };
+  union Half {
+    uint2 raw;
+    T v[N / 2];
+  };
+};
+
+template <typename E, bool kFp8>
+__device__ __forceinline__ void store_chunk(void* cache, uint64_t elem_off, const typename Vec<E>::Chunk& c,
+                                            float scale, float inv_scale) {
+  constexpr uint32_t N = Vec<E>::N;
+  if constexpr (kFp8) {
+    float x[N];
+#pragma unroll
+    for (uint32_t i = 0; i < N; ++i) x[i] = div_rn(E::to_f(c.v[i]), scale, inv_scale);
+    uint32_t w[N / 4];
+#pragma unroll
+    for (uint32_t i = 0; i < N / 4; ++i) w[i] = encode4_e4m3fn(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    if constexpr (N == 8) {
+      *reinterpret_cast<uint2*>(static_cast<uint8_t*>(cache) + elem_off) = uint2{w[0], w[1]};
+    } else {
+      *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(cache) + elem_off) = w[0];
+    }
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<typename E::T*>(cache) + elem_off) = c.raw;
+  }
+}
+
+template <typename E, bool kFp8, bool kNeox>
+__global__ __launch_bounds__(kRopeThreads) void rope_paged_kv_vec_kernel(RopeArgs a, uint32_t splits) {
+#pragma clang fp contract(off)
+  using T = typename E::T;
+  using V = Vec<E>;
+  constexpr uint32_t N = V::N;
+  const uint32_t token = blockIdx.x / splits;
+  const uint32_t split = blockIdx.x - token * splits;
+  const int64_t position = a.positions[token];
+  if (position < 0 || static_cast<uint64_t>(position) >= a.max_position) return;
+  const int64_t slot = token < a.cache_tokens ? a.slot_mapping[token] : -1;
+  const bool write = slot >= 0 && static_cast<uint64_t>(slot) < static_cast<uint64_t>(a.num_blocks) * a.block_size;
+  uint64_t kc_base = 0, vc_base = 0;
+  if (write) {
+    const uint64_t blk = static_cast<uint64_t>(slot) / a.block_size, page = static_cast<uint64_t>(slot) % a.block_size;
+    kc_base = blk * a.kc_block + page * a.kc_page;
+    vc_base = blk * a.vc_block + page * a.vc_page;
+  }
+  const uint32_t half = a.rotary_dim / 2U;
+  const uint32_t rot_items = kNeox ? half / N : a.rotary_dim / N;
+  const uint32_t tail_chunks = (a.head_size - a.rotary_dim) / N;
+  const uint32_t value_chunks = a.value_head_size / N;
+  const uint32_t q_items = a.query_heads * rot_items;
+  const uint32_t k_items = a.kv_heads * rot_items;
+  const uint32_t t_items = write ? a.kv_heads * tail_chunks : 0U;
+  const uint32_t v_items = write ? a.kv_heads * value_chunks : 0U;
+  const uint32_t total = q_items + k_items + t_items + v_items;
+  const T* cs = static_cast<const T*>(a.cos_sin) + static_cast<uint64_t>(position) * a.rotary_dim;
+  T* qrow = static_cast<T*>(a.query) + token * a.q_token;
+  T* krow = static_cast<T*>(a.key) + token * a.k_token;
+  const T* vrow = static_cast<const T*>(a.value) + token * a.v_token;
+
+  for (uint32_t base = split * kRopeThreads; base < total; base += splits * kRopeThreads * kVecUnroll) {
+    // Phase 1: decode items and issue every load.
+    uint32_t kind[kVecUnroll], head[kVecUnroll], c[kVecUnroll];
+    typename V::Chunk x1[kVecUnroll], x2[kVecUnroll], co[kVecUnroll], si[kVecUnroll];
+#pragma unroll
+    for (uint32_t u = 0; u < kVecUnroll; ++u) {
+      const uint32_t item = base + u * splits * kRopeThreads + threadIdx.x;
+      kind[u] = 4;  // none
+      head[u] = 0;
+      c[u] = 0;
+      if (item >= total) continue;
+      uint32_t r = item;
+      if (r < q_items) {
+        kind[u] = 0;
+      } else if ((r -= q_items) < k_items) {
+        kind[u] = 1;
+      } else if ((r -= k_items) < t_items) {
+        kind[u] = 2;
+      } else {
+        r -= t_items;
+        kind[u] = 3;
+      }
+      const uint32_t per = kind[u] <= 1 ? rot_items : (kind[u] == 2 ? tail_chunks : value_chunks);
+      head[u] = r / per;
+      c[u] = r - head[u] * per;
+      if (kind[u] <= 1) {
+        const T* row = kind[u] == 0 ? qrow + head[u] * a.q_head : krow + head[u] * a.k_head;
+        if constexpr (kNeox) {
+          x1[u].raw = *reinterpret_cast<const uint4*>(row + c[u] * N);
+          x2[u].raw = *reinterpret_cast<const uint4*>(row + half + c[u] * N);
+          co[u].raw = *reinterpret_cast<const uint4*>(cs + c[u] * N);
+          si[u].raw = *reinterpret_cast<const uint4*>(cs + half + c[u] * N);
+        } else {
+          x1[u].raw = *reinterpret_cast<const uint4*>(row + c[u] * N);
+          typename V::Half hc, hs;
+          hc.raw = *reinterpret_cast<const uint2*>(cs + c[u] * (N / 2));
+          hs.raw = *reinterpret_cast<const uint2*>(cs + half + c[u] * (N / 2));
+#pragma unroll
+          for (uint32_t i = 0; i < N / 2; ++i) {
+            co[u].v[i] = hc.v[i];
+            si[u].v[i] = hs.v[i];
+          }
+        }
+      } else if (kind[u] == 2) {
+        x1[u].raw = *reinterpret_cast<const uint4*>(krow + head[u] * a.k_head + a.rotary_dim + c[u] * N);
+      } else {
+        x1[u].raw = *reinterpret_cast<const uint4*>(vrow + head[u] * a.v_head + c[u] * N);
+      }
+    }
+    // Phase 2: rotate, write back, store to the caches.
+#pragma unroll
+    for (uint32_t u = 0; u < kVecUnroll; ++u) {
+      if (kind[u] == 4) continue;
+      const float kscale = kFp8 && kind[u] != 0 ? a.key_scales[static_cast<uint64_t>(head[u]) * a.scale_stride] : 1.0f;
+      const float kinv = 1.0f / kscale;
+      if (kind[u] <= 1) {
+        typename V::Chunk r1, r2;
+        if constexpr (kNeox) {
+#pragma unroll
+          for (uint32_t i = 0; i < N; ++i) {
+            const float f = E::to_f(x1[u].v[i]), s = E::to_f(x2[u].v[i]);
+            const float cc = E::to_f(co[u].v[i]), ss = E::to_f(si[u].v[i]);
+            r1.v[i] = E::from_f(f * cc - s * ss);
+            r2.v[i] = E::from_f(s * cc + f * ss);
+          }
+        } else {
+#pragma unroll
+          for (uint32_t i = 0; i < N / 2; ++i) {
+            const float f = E::to_f(x1[u].v[2 * i]), s = E::to_f(x1[u].v[2 * i + 1]);
+            const float cc = E::to_f(co[u].v[i]), ss = E::to_f(si[u].v[i]);
+            r1.v[2 * i] = E::from_f(f * cc - s * ss);
+            r1.v[2 * i + 1] = E::from_f(s * cc + f * ss);
+          }
+        }
+        T* row = kind[u] == 0 ? qrow + head[u] * a.q_head : krow + head[u] * a.k_head;
+        const uint32_t o1 = c[u] * N, o2 = half + c[u] * N;
+        *reinterpret_cast<uint4*>(row + o1) = r1.raw;
+        if constexpr (kNeox) *reinterpret_cast<uint4*>(row + o2) = r2.raw;
+        if (kind[u] == 1 && write) {
+          const uint64_t dst = kc_base + head[u] * a.kc_head;
+          store_chunk<E, kFp8>(a.key_cache, dst + o1, r1, kscale, kinv);
+          if constexpr (kNeox) store_chunk<E, kFp8>(a.key_cache, dst + o2, r2, kscale, kinv);
+        }
+      } else if (kind[u] == 2) {
+        store_chunk<E, kFp8>(a.key_cache, kc_base + head[u] * a.kc_head + a.rotary_dim + c[u] * N, x1[u], kscale,
+                             kinv);
+      } else {
+        const float vscale = kFp8 ? a.value_scales[static_cast<uint64_t>(head[u]) * a.scale_stride] : 1.0f;
+        store_chunk<E, kFp8>(a.value_cache, vc_base + head[u] * a.vc_head + c[u] * N, x1[u], vscale, 1.0f / vscale);
+      }
+    }
+  }
+}
+
 template <typename E>
 int rope_write(void* query, void* key, const void* value, const int64_t* positions, const void* cos_sin_cache,
                void* key_cache, void* value_cache, const float* key_scales, const float* value_scales,
@@ -212,6 +417,46 @@ int rope_write(void* query, void* key, const void* value, const int64_t* positio
                 key_cache_page_stride, key_cache_head_stride, value_cache_block_stride, value_cache_page_stride,
                 value_cache_head_stride};
   hipStream_t s = static_cast<hipStream_t>(stream);
+
+  // 16-byte vector path when every row, stride and base is chunk-aligned.
+  constexpr uint64_t N = Vec<E>::N;
+  const uint64_t cache_elem = fp8 ? 1 : sizeof(typename E::T);
+  auto aligned = [](const void* p, uint64_t bytes) { return reinterpret_cast<uintptr_t>(p) % bytes == 0; };
+  const bool vec_ok =
+      (is_neox ? (rotary_dim / 2) % N == 0 : rotary_dim % N == 0) && head_size % N == 0 &&
+      value_head_size % N == 0 && query_token_stride % N == 0 && query_head_stride % N == 0 &&
+      key_token_stride % N == 0 && key_head_stride % N == 0 && value_token_stride % N == 0 &&
+      value_head_stride % N == 0 && key_cache_block_stride % N == 0 && key_cache_page_stride % N == 0 &&
+      key_cache_head_stride % N == 0 && value_cache_block_stride % N == 0 && value_cache_page_stride % N == 0 &&
+      value_cache_head_stride % N == 0 && aligned(query, 16) && aligned(key, 16) && aligned(value, 16) &&
+      aligned(cos_sin_cache, 16) && aligned(key_cache, N * cache_elem) && aligned(value_cache, N * cache_elem);
+  const uint64_t rot_items = is_neox ? rotary_dim / 2 / N : rotary_dim / N;
+  const uint64_t max_items = static_cast<uint64_t>(query_heads) * rot_items +
+                             static_cast<uint64_t>(kv_heads) * (rot_items + (head_size - rotary_dim) / N +
+                                                                value_head_size / N);
+  if (vec_ok && max_items <= (1ULL << 31)) {
+    // Enough workgroups to cover the chip even for a decode step of a few tokens.
+    const uint64_t max_splits = (max_items + kRopeThreads - 1) / kRopeThreads;
+    uint64_t splits = (2048 + tokens - 1) / tokens;
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    const uint64_t vgroups = static_cast<uint64_t>(tokens) * splits;
+    if (vgroups <= static_cast<uint64_t>(std::numeric_limits<int>::max())) {
+      const dim3 grid(static_cast<uint32_t>(vgroups));
+      const uint32_t sp = static_cast<uint32_t>(splits);
+      if (fp8) {
+        if (is_neox) hipLaunchKernelGGL((rope_paged_kv_vec_kernel<E, true, true>), grid, dim3(kRopeThreads), 0, s, args, sp);
+        else hipLaunchKernelGGL((rope_paged_kv_vec_kernel<E, true, false>), grid, dim3(kRopeThreads), 0, s, args, sp);
+      } else {
+        if (is_neox) hipLaunchKernelGGL((rope_paged_kv_vec_kernel<E, false, true>), grid, dim3(kRopeThreads), 0, s, args, sp);
+        else hipLaunchKernelGGL((rope_paged_kv_vec_kernel<E, false, false>), grid, dim3(kRopeThreads), 0, s, args, sp);
+      }
+      if (hipGetLastError() != hipSuccess) return fail(LOOM_HIP_LAUNCH_ERROR, "RoPE+paged-KV kernel launch failed");
+      loom_hip_detail::count_launch(LOOM_HIP_ROPE_PAGED_KV_WRITE);
+      return LOOM_HIP_SUCCESS;
+    }
+  }
+
   if (fp8) {
     hipLaunchKernelGGL((rope_paged_kv_kernel<E, true>), dim3(static_cast<uint32_t>(groups)), dim3(kRopeThreads), 0,
                        s, args);

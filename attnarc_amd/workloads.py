@@ -276,3 +276,92 @@ def run_case(case: DecodeCase, *, output=None, lse=None, workspace=None, return_
         partition_tokens=case.partition_tokens, output=output, lse=lse, workspace=workspace,
         return_lse=return_lse,
     )
+
+
+# ---------------------------------------------------------------------------
+# RoPE + paged K/V write workloads
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class RopeWriteCase:
+    """Inputs of one fused RoPE + paged-KV write call (``ops.rope_paged_kv_write_``)."""
+
+    name: str
+    dtype: torch.dtype
+    cache_encoding: str  # "native" or "fp8"
+    layout: str  # "NHD" or "HND"
+    query: torch.Tensor  # [T, Hq, D]
+    key: torch.Tensor  # [T, Hkv, D]
+    value: torch.Tensor  # [T, Hkv, D]
+    positions: torch.Tensor  # [T] int64
+    cos_sin_cache: torch.Tensor  # [max_position, rotary_dim]
+    kv_cache: torch.Tensor  # [blocks, 2, block_size, Hkv, D] (NHD or HND strides)
+    key_scales: torch.Tensor
+    value_scales: torch.Tensor
+    slot_mapping: torch.Tensor  # [T] int64
+    is_neox: bool = True
+
+    @property
+    def tokens(self) -> int:
+        return int(self.query.shape[0])
+
+    def algorithmic_bytes(self) -> int:
+        """HBM bytes one call must move: Q and K read and written back, V,
+        positions, slots and the cos/sin row read, K and V cache rows written."""
+        t, hq, d = self.query.shape
+        hkv = self.key.shape[1]
+        e = self.query.element_size()
+        ce = self.kv_cache.element_size()
+        rd = self.cos_sin_cache.shape[1]
+        return t * (2 * (hq + hkv) * d * e + hkv * d * e + 16 + rd * e + 2 * hkv * d * ce)
+
+    def args(self):
+        return (self.query, self.key, self.value, self.positions, self.cos_sin_cache, self.kv_cache,
+                self.key_scales, self.value_scales, self.slot_mapping, self.is_neox)
+
+    def describe(self) -> dict:
+        return {
+            "workload": self.name,
+            "tokens": self.tokens,
+            "query_heads": int(self.query.shape[1]),
+            "kv_heads": int(self.key.shape[1]),
+            "head_size": int(self.query.shape[2]),
+            "rotary_dim": int(self.cos_sin_cache.shape[1]),
+            "dtype": str(self.dtype).replace("torch.", ""),
+            "cache_encoding": self.cache_encoding,
+            "layout": self.layout,
+            "block_size": int(self.kv_cache.shape[2]),
+            "num_blocks": int(self.kv_cache.shape[0]),
+        }
+
+
+def rope_write_case(tokens: int, device, *, query_heads=32, kv_heads=8, head_size=128, rotary_dim=128,
+                    max_position=8192, block_size=16, dtype=torch.bfloat16, cache_encoding="fp8", layout="HND",
+                    seed: int = 7, name: str | None = None) -> RopeWriteCase:
+    """Llama-3-8B-shaped write: ``tokens`` new tokens into a pool of 4x that many slots."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = _randn((tokens, query_heads, head_size), gen, device, dtype)
+    k = _randn((tokens, kv_heads, head_size), gen, device, dtype)
+    v = _randn((tokens, kv_heads, head_size), gen, device, dtype)
+    positions = torch.randint(0, max_position, (tokens,), generator=gen, device=device)
+    inv = 1.0 / (10000 ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32, device=device) / rotary_dim))
+    freqs = torch.outer(torch.arange(max_position, dtype=torch.float32, device=device), inv)
+    cs = torch.cat((freqs.cos(), freqs.sin()), dim=-1).to(dtype)
+    num_blocks = max(1, -(-4 * tokens // block_size))
+    slots = torch.randperm(num_blocks * block_size, generator=gen, device=device)[:tokens].to(torch.int64)
+    cache_dtype = torch.uint8 if cache_encoding == "fp8" else dtype
+    shape = (num_blocks, 2, block_size, kv_heads, head_size)
+    part = block_size * kv_heads * head_size
+    if layout == "NHD":
+        kv = torch.zeros(shape, device=device, dtype=cache_dtype)
+    else:
+        kv = torch.zeros(num_blocks * 2 * part, device=device, dtype=cache_dtype).as_strided(
+            shape, (2 * part, part, head_size, block_size * head_size, 1))
+    ks = torch.full((kv_heads,), 0.05, device=device)
+    vs = torch.full((kv_heads,), 0.05, device=device)
+    return RopeWriteCase(
+        name=name or f"rope-kv-write T{tokens} Hq{query_heads}/Hkv{kv_heads} D{head_size} "
+                     f"{str(dtype).replace('torch.', '')}->{cache_encoding} {layout}",
+        dtype=dtype, cache_encoding=cache_encoding, layout=layout, query=q, key=k, value=v, positions=positions,
+        cos_sin_cache=cs, kv_cache=kv, key_scales=ks, value_scales=vs, slot_mapping=slots)

@@ -164,6 +164,111 @@ def cpu_baseline(case, budget_s: float = 15.0):
     }
 
 
+def _time_calls(fn, steps):
+    import torch
+
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def rope_cpu_baseline(case, budget_s: float):
+    """Time the oracle's fused write on growing token prefixes (kind 'port')."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    from gpu_util import ORACLE_DTYPE, to_host
+
+    oracle.lib()
+    t, hq, d = case.query.shape
+    hkv = case.key.shape[1]
+    nb, bs = case.kv_cache.shape[0], case.kv_cache.shape[2]
+    q, k, v = to_host(case.query), to_host(case.key), to_host(case.value)
+    pos, cs, slots = to_host(case.positions), to_host(case.cos_sin_cache), to_host(case.slot_mapping)
+    fp8 = case.cache_encoding == "fp8"
+    cdt = np.uint8 if fp8 else k.dtype
+    kc = np.zeros(nb * bs * hkv * d, cdt)
+    vc = np.zeros(nb * bs * hkv * d, cdt)
+    kw = dict(key_scales=case.key_scales.cpu().numpy(), value_scales=case.value_scales.cpu().numpy()) if fp8 else {}
+    n, elapsed = 64, 0.0
+    while True:
+        n = min(n, t)
+        rot = oracle.rotary_spec_new(n, hq, hkv, d, cs.shape[1], cs.shape[0], ORACLE_DTYPE[case.dtype], oracle.NEOX)
+        spec = oracle.rope_write_spec_new(rot, d, nb, bs, oracle.FP8_E4M3 if fp8 else oracle.NATIVE,
+                                          oracle.PER_HEAD if case.key_scales.numel() > 1 else oracle.PER_TENSOR)
+        # The oracle copies the caches it writes; time that copy separately and subtract it.
+        c0 = time.perf_counter()
+        kc.copy(), vc.copy()
+        copy_s = time.perf_counter() - c0
+        t0 = time.perf_counter()
+        oracle.rope_paged_kv_write(q[:n], k[:n], v[:n], pos[:n], cs, kc, vc, slots[:n], spec, **kw)
+        elapsed = max(time.perf_counter() - t0 - copy_s, 1e-9)
+        if elapsed >= budget_s or n == t:
+            break
+        n = min(t, int(n * max(2.0, budget_s / elapsed * 0.9)))
+    per_token = case.algorithmic_bytes() / t
+    return {
+        "value": n * per_token / elapsed / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"first {n} of {t} tokens of the same workload ({elapsed:.1f} s, single-threaded C++ oracle, "
+                  f"cache-copy time excluded; host nproc={os.cpu_count()})",
+    }
+
+
+def bench_rope(args, dev) -> int:
+    """One step = one fused RoPE + paged-KV write over the whole token batch."""
+    import torch
+
+    from attnarc_amd import ops, workloads
+
+    log(f"[bench] building rope-kv-write inputs ({args.rope_tokens} tokens)")
+    case = workloads.rope_write_case(args.rope_tokens, dev, cache_encoding=args.rope_cache)
+    nbytes = case.algorithmic_bytes()
+    step = lambda: ops.rope_paged_kv_write_(*case.args())  # noqa: E731
+    for _ in range(args.warmup):
+        step()
+    ms = _time_calls(step, args.steps)
+    # Decode-step latency: one token per sequence for a batch of 64 sequences.
+    small = workloads.rope_write_case(64, dev, cache_encoding=args.rope_cache, seed=8)
+    small_step = lambda: ops.rope_paged_kv_write_(*small.args())  # noqa: E731
+    for _ in range(10):
+        small_step()
+    small_us = _time_calls(small_step, 200) * 1e3
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else rope_cpu_baseline(case, args.cpu_budget)
+    print(json.dumps({
+        "metric": "fused RoPE + paged-KV write HBM GB/s, 1xMI355X",
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_call": round(ms * 1e3, 2),
+        "us_per_call_decode_step_64_tokens": round(small_us, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": str(case.dtype).replace("torch.", ""),
+        "data": "synthetic (seeded N(0,1) Q/K/V, random positions, unique random slots in a 4x pool)",
+        "config": {**case.describe(), "bytes_per_call": nbytes, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "kernel": "rope_paged_kv_kernel"},
+        "cpu_baseline": cpu,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -177,6 +282,10 @@ def main() -> int:
                     help="override the configuration's cache layout (same logical data)")
     ap.add_argument("--partition", type=int, default=None,
                     help="override the configuration's split-K partition size (tokens; 0 = one partition)")
+    ap.add_argument("--op", choices=["decode", "rope"], default="decode",
+                    help="decode: paged decode attention (the metric); rope: fused RoPE + paged-KV write")
+    ap.add_argument("--rope-tokens", type=int, default=32768)
+    ap.add_argument("--rope-cache", choices=["fp8", "native"], default="fp8")
     ap.add_argument("--probe", choices=["read", "copy", "gather"], default=None,
                     help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
@@ -207,6 +316,8 @@ def main() -> int:
     if args.probe:
         print(json.dumps({"probe": args.probe, "bytes": 4 << 30, "GB/s": round(hbm_probe(args.probe), 1)}))
         return 0
+    if args.op == "rope":
+        return bench_rope(args, dev)
     log(f"[bench] building config {args.config} inputs")
     case = workloads.config(args.config, dev, layout=args.layout)
     if args.partition is not None:

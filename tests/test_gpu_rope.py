@@ -90,9 +90,14 @@ def random_slots(tokens, capacity, gen, pad_every=4):
 
 
 def check_case(dtype, layout, encoding, is_neox, T, Hq, Hkv, D, rd, maxpos, NB, bs, seed, cache_tokens=None,
-               big_heads=False):
+               big_heads=False, misalign=False):
     gen = torch.Generator().manual_seed(seed)
     q = torch.randn((T, Hq, D), generator=gen).to(dtype).to(DEV)
+    if misalign:
+        # A query view one element off 16-byte alignment takes the general (per-element) kernel.
+        buf = torch.empty(q.numel() + 1, device=DEV, dtype=dtype)
+        buf[1:].copy_(q.reshape(-1))
+        q = buf[1:].view(T, Hq, D)
     k = torch.randn((T, Hkv, D), generator=gen)
     if big_heads:
         k[:, 0] *= 300.0  # saturates FP8 with scale < 1
@@ -140,6 +145,22 @@ def test_llama_shape_matches_oracle(dtype, layout, encoding):
     # Llama-3-8B decode step: 32 query heads, 8 KV heads, full 128-dim rotary.
     check_case(dtype, layout, encoding, True, T=64, Hq=32, Hkv=8, D=128, rd=128, maxpos=8192, NB=64, bs=16,
                seed=11)
+
+
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("encoding", ["native", "per-head"])
+def test_unaligned_views_match_oracle(is_neox, encoding):
+    check_case(torch.bfloat16, "NHD", encoding, is_neox, T=32, Hq=32, Hkv=8, D=128, rd=128, maxpos=4096, NB=16,
+               bs=16, seed=12, misalign=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("is_neox", [True, False])
+@pytest.mark.parametrize("encoding", ["native", "per-tensor"])
+def test_vector_path_partial_rotary_and_tail(dtype, is_neox, encoding):
+    # rotary 64 of 192 dims: vector rotary items, tail chunks and value chunks all active.
+    check_case(dtype, "HND", encoding, is_neox, T=40, Hq=6, Hkv=2, D=192, rd=64, maxpos=300, NB=24, bs=8, seed=9,
+               cache_tokens=33, big_heads=True)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -226,8 +247,9 @@ def test_packed_qkv_and_short_slot_mapping(cache):
     assert_bits(kv[:, 1], exp[3], "value cache")
 
 
-@pytest.mark.parametrize("scale", [1.0, 0.37, 3.0e-3])
-def test_fp8_encoding_sweep_is_exact(scale):
+@pytest.mark.parametrize("scale", [1.0, 0.37, 3.0e-3, 1.7e-38])
+@pytest.mark.parametrize("rotary_dim", [2, 8])  # 2: general kernel; 8: 16-byte vector kernel
+def test_fp8_encoding_sweep_is_exact(scale, rotary_dim):
     """Every FP8 rounding boundary, saturation, NaN/inf, signed zero and F32
     subnormals pass through the device encoder (F32 V rows: no source rounding)."""
     codes = np.arange(0x7F, dtype=np.uint8)
@@ -246,7 +268,7 @@ def test_fp8_encoding_sweep_is_exact(scale):
     q = torch.zeros((T, 1, D), device=DEV)
     k = torch.zeros((T, 1, D), device=DEV)
     pos = torch.zeros(T, dtype=torch.int64, device=DEV)
-    cs = cos_sin_cache(1, 2, torch.float32)
+    cs = cos_sin_cache(1, rotary_dim, torch.float32)
     kv = packed_cache(T, 1, 1, D, torch.uint8, "NHD")
     slots = torch.arange(T, device=DEV)
     st = torch.tensor([scale], dtype=torch.float32, device=DEV)
@@ -379,3 +401,27 @@ def test_write_then_decode_round_trip(encoding):
                         key_layout=oracle.CacheLayout.nhd(bs, Hkv, D), value_layout=oracle.CacheLayout.nhd(bs, Hkv, D),
                         **kw)
     assert_parity(out, oracle.bf16_bits_to_f32(ref).astype(np.float64).reshape(B, Hq, D), dtype, "round trip")
+
+
+@pytest.mark.parametrize("rotary_dim", [2, 8])
+def test_fp8_random_magnitudes_and_scales_are_exact(rotary_dim):
+    """One million log-uniform F32 values over the whole E4M3 range (and past
+    both ends) with random per-head scales: the device's division and
+    conversion must give the oracle's bytes for every one."""
+    rng = np.random.default_rng(2024)
+    T, H, D = 4096, 4, 64
+    mag = np.exp2(rng.uniform(-16, 12, size=(T, H, D))) * rng.choice([-1.0, 1.0], size=(T, H, D))
+    v = torch.from_numpy(mag.astype(np.float32)).to(DEV)
+    q = torch.zeros((T, 1, D), device=DEV)
+    k = torch.from_numpy((mag[::-1].copy() * 0.75).astype(np.float32)).to(DEV)
+    pos = torch.zeros(T, dtype=torch.int64, device=DEV)
+    cs = cos_sin_cache(1, rotary_dim, torch.float32)
+    kv = packed_cache(T // 4, 4, H, D, torch.uint8, "HND")
+    slots = torch.from_numpy(rng.permutation(T)).to(DEV)
+    ks = torch.from_numpy(np.exp2(rng.uniform(-8, 8, H)).astype(np.float32)).to(DEV)
+    vs = torch.from_numpy(np.exp2(rng.uniform(-8, 8, H)).astype(np.float32)).to(DEV)
+    exp = oracle_write(q, k, v, pos, cs, kv, slots, True, ks, vs)
+    ops.rope_paged_kv_write_(q, k, v, pos, cs, kv, ks, vs, slots, True)
+    torch.cuda.synchronize()
+    assert_bits(kv[:, 0], exp[2], "key cache")
+    assert_bits(kv[:, 1], exp[3], "value cache")
