@@ -28,7 +28,7 @@ KV_CACHE_FP8_E4M3 = 1
 F32, F16, BF16 = 0, 1, 2
 ROPE_PAGED_KV_WRITE = 5
 PAGED_DECODE_ATTENTION = 9
-KERNEL_DECODE, KERNEL_MERGE = 0, 1
+KERNEL_DECODE, KERNEL_MERGE, KERNEL_ROPE = 0, 1, 2
 
 P = ctypes.c_void_p
 U32 = ctypes.c_uint32

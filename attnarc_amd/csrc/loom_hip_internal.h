@@ -18,6 +18,19 @@ int device_available();
 // Counts one successful submission of `operation` (a LoomHipOperator id).
 void count_launch(uint32_t operation);
 
+// While kernel timing is enabled, brackets the launches made during its
+// lifetime with events on `stream`, accounted to `kernel` (a LoomHipKernel id).
+class KernelTimer {
+ public:
+  KernelTimer(int kernel, void* stream);
+  ~KernelTimer();
+  KernelTimer(const KernelTimer&) = delete;
+  KernelTimer& operator=(const KernelTimer&) = delete;
+
+ private:
+  void* impl_;
+};
+
 }  // namespace loom_hip_detail
 
 #endif  // LOOM_HIP_INTERNAL_H_

@@ -1538,12 +1538,14 @@ int fail(int status, const char* message) {
   return status;
 }
 
+constexpr int kTimedKernels = 3;  // LOOM_HIP_KERNEL_DECODE, _MERGE, _ROPE
+
 struct TimingState {
   std::mutex mu;
-  bool enabled = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[2];
-  double total_ms[2] = {0.0, 0.0};
-  uint64_t launches[2] = {0, 0};
+  std::atomic<bool> enabled{false};
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending[kTimedKernels];
+  double total_ms[kTimedKernels] = {};
+  uint64_t launches[kTimedKernels] = {};
 };
 
 TimingState& timing() {
@@ -2081,6 +2083,13 @@ void count_launch(uint32_t operation) {
   if (operation == LOOM_HIP_ROPE_PAGED_KV_WRITE) g_rope_launches.fetch_add(1, std::memory_order_relaxed);
 }
 
+KernelTimer::KernelTimer(int kernel, void* stream)
+    : impl_(timing().enabled.load(std::memory_order_relaxed)
+                ? new TimedLaunch(kernel, static_cast<hipStream_t>(stream))
+                : nullptr) {}
+
+KernelTimer::~KernelTimer() { delete static_cast<TimedLaunch*>(impl_); }
+
 }  // namespace loom_hip_detail
 
 // ===========================================================================
@@ -2129,7 +2138,7 @@ int loom_hip_kernel_timing_enable(uint32_t enable) {
   TimingState& t = timing();
   std::lock_guard<std::mutex> lock(t.mu);
   t.enabled = enable != 0;
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < kTimedKernels; ++k) {
     for (auto& e : t.pending[k]) {
       (void)hipEventSynchronize(e.second);
       (void)hipEventDestroy(e.first);
@@ -2143,7 +2152,7 @@ int loom_hip_kernel_timing_enable(uint32_t enable) {
 }
 
 int loom_hip_kernel_timing_read(uint32_t kernel, double* total_ms, uint64_t* launches) {
-  if (kernel > 1 || total_ms == nullptr || launches == nullptr)
+  if (kernel >= static_cast<uint32_t>(kTimedKernels) || total_ms == nullptr || launches == nullptr)
     return fail(LOOM_HIP_INVALID_ARGUMENT, "unknown kernel id or null output");
   TimingState& t = timing();
   std::lock_guard<std::mutex> lock(t.mu);

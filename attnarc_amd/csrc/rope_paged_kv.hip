@@ -417,6 +417,7 @@ int rope_write(void* query, void* key, const void* value, const int64_t* positio
                 key_cache_page_stride, key_cache_head_stride, value_cache_block_stride, value_cache_page_stride,
                 value_cache_head_stride};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  loom_hip_detail::KernelTimer timed(LOOM_HIP_KERNEL_ROPE, stream);
 
   // 16-byte vector path when every row, stride and base is chunk-aligned.
   constexpr uint64_t N = Vec<E>::N;

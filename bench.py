@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c3_traffic.json")
+ROPE_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "rope_kv_write_traffic.json")
 
 
 def log(msg: str) -> None:
@@ -243,18 +244,45 @@ def bench_rope(args, dev) -> int:
     for _ in range(10):
         small_step()
     small_us = _time_calls(small_step, 200) * 1e3
-    achieved = nbytes / (ms * 1e-3) / 1e9
+    value = nbytes / (ms * 1e-3) / 1e9
+    # Kernel duration from events the library records on the launch stream.
+    from attnarc_amd import _native
+
+    ops.kernel_timing_enable(True)
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    k_ms, k_n = ops.kernel_timing_read(_native.KERNEL_ROPE)
+    small_step()
+    torch.cuda.synchronize()
+    ops.kernel_timing_read(_native.KERNEL_ROPE)
+    ops.kernel_timing_enable(True)
+    for _ in range(50):
+        small_step()
+    torch.cuda.synchronize()
+    s_ms, s_n = ops.kernel_timing_read(_native.KERNEL_ROPE)
+    ops.kernel_timing_enable(False)
+    kernel_us = k_ms / max(k_n, 1) * 1e3
+    small_kernel_us = s_ms / max(s_n, 1) * 1e3
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
     cpu = None if args.no_cpu_baseline else rope_cpu_baseline(case, args.cpu_budget)
+    traffic = None
+    if os.path.exists(ROPE_TRAFFIC_FILE):
+        with open(ROPE_TRAFFIC_FILE) as f:
+            t = json.load(f)
+        traffic = t.get("bytes_per_launch", {}).get(case.name)
     print(json.dumps({
         "metric": "fused RoPE + paged-KV write HBM GB/s, 1xMI355X",
-        "value": round(achieved, 2),
+        "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
         "us_per_call": round(ms * 1e3, 2),
+        "kernel_us": round(kernel_us, 2),
         "us_per_call_decode_step_64_tokens": round(small_us, 2),
+        "kernel_us_decode_step_64_tokens": round(small_kernel_us, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -262,8 +290,8 @@ def bench_rope(args, dev) -> int:
         "data": "synthetic (seeded N(0,1) Q/K/V, random positions, unique random slots in a 4x pool)",
         "config": {**case.describe(), "bytes_per_call": nbytes, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "rope_paged_kv_kernel"},
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                     "kernel": "rope_paged_kv_vec_kernel"},
         "cpu_baseline": cpu,
     }), flush=True)
     return 0

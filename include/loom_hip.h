@@ -67,6 +67,7 @@ enum LoomHipOperator {
 enum LoomHipKernel {
   LOOM_HIP_KERNEL_DECODE = 0, /* per-(sequence, KV head, partition) kernel */
   LOOM_HIP_KERNEL_MERGE = 1,  /* split-K log-sum-exp merge kernel */
+  LOOM_HIP_KERNEL_ROPE = 2,   /* fused RoPE + paged-KV write kernel */
 };
 
 /* Replaces loom_cuda_status_string (rms_norm.cu:170-185). */
