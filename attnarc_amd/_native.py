@@ -30,6 +30,10 @@ ROPE_PAGED_KV_WRITE = 5
 PAGED_DECODE_ATTENTION = 9
 KERNEL_DECODE, KERNEL_MERGE, KERNEL_ROPE = 0, 1, 2
 
+# Bridge status codes (include/loom_hip_bridge.h); they differ from the
+# unchecked library's codes above, as loom_cuda_bridge.h's do from loom_cuda.h's.
+BRIDGE_SUCCESS, BRIDGE_INVALID_ARGUMENT, BRIDGE_LAUNCH_ERROR, BRIDGE_UNAVAILABLE = 0, 1, 2, 3
+
 P = ctypes.c_void_p
 U32 = ctypes.c_uint32
 U64 = ctypes.c_uint64
@@ -40,6 +44,9 @@ _BASE = [P, P, P, P, P, P] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _SPLIT = [P, P, P, P, P, P, P, U64] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _EXT = [P, P, P, P, P, P, P, P, P, P, U64] + [U32] * 9 + [U64] * 6 + [U32, U32, U32, F, P]
 _ROPE = [P] * 10 + [U32] * 12 + [U64] * 12 + [U32, P]
+# Checked bridge (include/loom_hip_bridge.h).
+_BRIDGE_ROPE = [U32, U32] + [P, U64] * 10 + [U32] * 10 + [U64] * 12 + [U32, P]
+_BRIDGE_DECODE = [U32] + [P, U64] * 7 + [U32] * 7 + [U64, U64, U32, U32, F, P]
 SIGNATURES = {
     "loom_hip_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "loom_hip_paged_decode_attention_f32": (_BASE, ctypes.c_int),
@@ -61,6 +68,13 @@ SIGNATURES = {
     "loom_hip_rope_paged_kv_write_f16": (_ROPE, ctypes.c_int),
     "loom_hip_rope_paged_kv_write_bf16": (_ROPE, ctypes.c_int),
     "loom_hip_backend_name": ([], ctypes.c_char_p),
+    "loom_hip_bridge_abi_version": ([], U32),
+    "loom_hip_bridge_last_error_message": ([], ctypes.c_char_p),
+    "loom_hip_bridge_launch_count": ([U32, ctypes.POINTER(U64)], ctypes.c_int),
+    "loom_hip_bridge_reset_launch_count": ([U32], ctypes.c_int),
+    "loom_hip_bridge_rope_paged_kv_write": (_BRIDGE_ROPE, ctypes.c_int),
+    "loom_hip_bridge_paged_decode_workspace_elements": ([U32] * 10 + [F, ctypes.POINTER(U64)], ctypes.c_int),
+    "loom_hip_bridge_paged_decode_attention": (_BRIDGE_DECODE, ctypes.c_int),
     "loom_hip_abi_version": ([], U32),
     "loom_hip_last_error_message": ([], ctypes.c_char_p),
     "loom_hip_launch_count": ([U32, ctypes.POINTER(U64)], ctypes.c_int),

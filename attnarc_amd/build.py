@@ -15,6 +15,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 SOURCES = [
     os.path.join(PKG_DIR, "csrc", "paged_decode_attention.hip"),
     os.path.join(PKG_DIR, "csrc", "rope_paged_kv.hip"),
+    os.path.join(PKG_DIR, "csrc", "loom_hip_bridge.cpp"),
 ]
 LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip.so")
 PROBE_SOURCE = os.path.join(PKG_DIR, "csrc", "hbm_probe.hip")
@@ -43,10 +44,41 @@ def _compile(sources, out: str, verbose: bool) -> None:
     os.replace(tmp, out)
 
 
+ADAPTER_SOURCES = [
+    os.path.join(PKG_DIR, "csrc", "torch_adapter", name)
+    for name in ("torch_ops.cpp", "attention.cpp", "rope_kv.cpp")
+]
+ADAPTER_LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip_torch.so")
+
+
+def _compile_adapter(verbose: bool) -> None:
+    """Host-only PyTorch Stable-ABI adapter, linked against libloom_hip.so."""
+    import torch.utils.cpp_extension as ext
+
+    torch_lib = ext.library_paths()[0]
+    tmp = ADAPTER_LIB_PATH + ".tmp"
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+        "-DUSE_ROCM",  # exposes the shim's aoti_torch_get_current_cuda_stream on ROCm builds
+        *[f"-I{p}" for p in ext.include_paths()],
+        f"-I{os.path.join(REPO_DIR, 'include')}",
+        *ADAPTER_SOURCES,
+        f"-L{os.path.dirname(LIB_PATH)}", "-lloom_hip",
+        f"-L{torch_lib}", "-ltorch_hip", "-ltorch_cpu", "-lc10",
+        "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}",
+        "-o", tmp,
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, ADAPTER_LIB_PATH)
+
+
 def build(verbose: bool = False) -> str:
-    """Compile the decode library and the HBM probe library; returns the former's path."""
+    """Compile the kernel library, the HBM probe library and the torch adapter; returns the first's path."""
     _compile(SOURCES, LIB_PATH, verbose)
     _compile([PROBE_SOURCE], PROBE_LIB_PATH, verbose)
+    _compile_adapter(verbose)
     return LIB_PATH
 
 

@@ -19,11 +19,11 @@ import torch
 from attnarc_amd import _native, ops
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "loom_hip.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("loom_hip.h", "loom_hip_bridge.h")]
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = "\n".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(loom_hip_[a-z0-9_]+)\s*\(", text)))
 
