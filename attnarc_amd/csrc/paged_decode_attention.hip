@@ -69,7 +69,7 @@ struct DecodeArgs {
   void* output;
   float* lse;
   float* ws_ml;  // [rows][parts][2] = (m in log2 units, l)
-  float* ws_o;   // [rows][parts][Dv], unnormalised, relative to m
+  void* ws_o;    // [rows][parts][Dv] partial outputs (PartialOut<QE> encoding)
   uint64_t k_block, k_page, k_head;  // element strides of the key cache
   uint64_t v_block, v_page, v_head;  // element strides of the value cache
   uint32_t query_heads;
@@ -146,6 +146,52 @@ __device__ __forceinline__ void wave_fence_lds() { asm volatile("" ::: "memory")
 
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maxima).
 __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Split-K partial outputs. F32 queries keep the unnormalised F32 sum
+// O_p = sum_t 2^(s_t - m_p) v_t. 16-bit queries store o_p = O_p / l_p in the
+// query's own type: half the bytes of the (write-heavy) partial states, and
+// o_p is a convex combination of V rows, so it stays in range; the merge
+// weights it by l_p again. The workspace keeps its F32 element count.
+template <typename QE>
+struct PartialOut {
+  static constexpr bool kNormalised = true;
+  using T = uint16_t;
+};
+template <>
+struct PartialOut<F32Elem> {
+  static constexpr bool kNormalised = false;
+  using T = float;
+};
+
+// Elements between consecutive partial rows: Dv, rounded up to even for
+// 16-bit partials so the merge can read dim pairs as aligned 4-byte words.
+template <typename QE>
+__host__ __device__ __forceinline__ uint32_t partial_stride(uint32_t dv) {
+  return PartialOut<QE>::kNormalised ? (dv + 1U) & ~1U : dv;
+}
+
+template <typename QE>
+__device__ __forceinline__ void put_partial(const DecodeArgs& a, uint64_t idx, float o, float inv_l) {
+  if constexpr (PartialOut<QE>::kNormalised) {
+    static_cast<uint16_t*>(a.ws_o)[idx] = QE::from_f(o * inv_l);
+  } else {
+    static_cast<float*>(a.ws_o)[idx] = o;
+  }
+}
+
+// Four consecutive dims of one partial row (idx a multiple of 4).
+template <typename QE>
+__device__ __forceinline__ void put_partial4(const DecodeArgs& a, uint64_t idx, f32x4 o, float scale, float inv_l) {
+  if constexpr (PartialOut<QE>::kNormalised) {
+    const float k = scale * inv_l;
+    const uint32_t w0 = QE::from_f(o[0] * k) | (static_cast<uint32_t>(QE::from_f(o[1] * k)) << 16);
+    const uint32_t w1 = QE::from_f(o[2] * k) | (static_cast<uint32_t>(QE::from_f(o[3] * k)) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ws_o) + idx) = make_uint2(w0, w1);
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(a.ws_o) + idx) =
+        make_float4(o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // General kernel: any head size, dtype, stride and group size.
@@ -283,7 +329,7 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
       const uint64_t state = row * a.parts + part;
-      a.ws_o[state * Dv + d] = O;
+      put_partial<QE>(a, state * partial_stride<QE>(Dv) + d, O, 1.0f / L);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
         a.ws_ml[state * 2 + 1] = L;
@@ -291,6 +337,7 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
     }
   }
 }
+
 
 // ---------------------------------------------------------------------------
 // Matrix-core kernel.
@@ -780,13 +827,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
         if (a.lse != nullptr && dec.g == 0) a.lse[row] = (M + log2f(L)) * kLn2;
       } else {
         const uint64_t state = row * a.parts + part;
-        float* o = a.ws_o + state * kDim + 4 * dec.g;
+        const float inv_l = 1.0f / L;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          *reinterpret_cast<float4*>(o + dt * 16) =
-              make_float4(dec.acc[ht][dt][0] * v_scale, dec.acc[ht][dt][1] * v_scale,
-                          dec.acc[ht][dt][2] * v_scale, dec.acc[ht][dt][3] * v_scale);
-        }
+        for (int dt = 0; dt < 8; ++dt)
+          put_partial4<QE>(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
         if (dec.g == 0) {
           a.ws_ml[state * 2] = M;
           a.ws_ml[state * 2 + 1] = L;
@@ -836,7 +880,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
         if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
       } else {
         const uint64_t state = row * a.parts + part;
-        a.ws_o[state * kDim + d] = O;
+        put_partial<QE>(a, state * kDim + d, O, 1.0f / L);
         if (d == 0) {
           a.ws_ml[state * 2] = M;
           a.ws_ml[state * 2 + 1] = L;
@@ -877,8 +921,9 @@ constexpr uint32_t kStepTileBytes = kStep * kTileRowBytes;  // 4 KiB
 // rows): chunk ch sits at ch ^ 2 (t & 7). The transposed reads fetch 8 bytes
 // per lane from rows 4g .. 4g + 3 for two lane groups g at a time; XORing
 // with three row bits spreads those eight rows over all 64 banks.
+template <uint32_t kPitch = kTileRowBytes>
 __device__ __forceinline__ uint32_t vtile_off(uint32_t t, uint32_t ch) {
-  return t * kTileRowBytes + ((ch ^ ((t & 7U) << 1)) << 4);
+  return t * kPitch + ((ch ^ ((t & 7U) << 1)) << 4);
 }
 
 template <int N>
@@ -901,6 +946,7 @@ __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_wait
 
 template <typename QE, bool kFp8>
 struct StreamDecoder {
+  static constexpr uint32_t kPitch = kTileRowBytes;  // bytes between consecutive tokens' rows in a stage
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
@@ -1002,7 +1048,7 @@ struct StreamDecoder {
       return Ops::from_fp8(w.x, w.y);
     } else {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ c;
-      return *reinterpret_cast<const vec8*>(stage + c * kTileRowBytes + chunk * 16);
+      return *reinterpret_cast<const vec8*>(stage + c * kPitch + chunk * 16);
     }
   }
 
@@ -1044,7 +1090,7 @@ struct StreamDecoder {
     if (t0 + kStep <= len) return;  // uniform
     const uint32_t t = lane >> 2;   // 4 lanes per row, 64 bytes each
     if (t0 + t >= len) {
-      u32x4* row = reinterpret_cast<u32x4*>(tile + t * kTileRowBytes + (lane & 3U) * 64);
+      u32x4* row = reinterpret_cast<u32x4*>(tile + t * kPitch + (lane & 3U) * 64);
 #pragma unroll
       for (int i = 0; i < 4; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
     }
@@ -1082,7 +1128,7 @@ struct StreamDecoder {
     lds_u8* base = (lds_u8*)tile;
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; ++dt) {
-      const uint32_t off = vtile_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
+      const uint32_t off = vtile_off<kPitch>(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
       const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
       acc[dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb, acc[dt]);
     }
@@ -1174,18 +1220,47 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   return it;
 }
 
+// One wave's result for its KV head's query group: the normalised output
+// (and LSE) when the sequence is one partition, else the partition's
+// partial output (PartialOut encoding) and (m, l) in the split-K workspace. Lane (g, c) holds dims
+// dt*16 + 4g .. +3 of head c; only lanes of live heads call this.
+template <typename QE, typename Dec>
+__device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec& dec, uint32_t seq, uint32_t kvh,
+                                                  uint32_t part, float v_scale, float l) {
+  const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + dec.c;
+  if (a.parts == 1) {
+    const float inv = v_scale / l;
+    uint16_t* o = static_cast<uint16_t*>(a.output) + row * kDim + 4 * dec.g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      uint32_t w0 = QE::from_f(dec.acc[dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][1] * inv)) << 16);
+      uint32_t w1 = QE::from_f(dec.acc[dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][3] * inv)) << 16);
+      *reinterpret_cast<uint2*>(o + dt * 16) = make_uint2(w0, w1);
+    }
+    if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m + log2f(l)) * kLn2;
+  } else {
+    const uint64_t state = row * a.parts + part;
+    const float inv_l = 1.0f / l;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) put_partial4<QE>(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[dt], v_scale, inv_l);
+    if (dec.g == 0) {
+      a.ws_ml[state * 2] = dec.m;
+      a.ws_ml[state * 2 + 1] = l;
+    }
+  }
+}
+
+constexpr int kStreamStages = 2;  // pipeline stages (deeper pipelines measured no faster)
+
+// One work item of the streaming kernel, from its first loads to its
+// partial-state stores. `tiles` holds kSplit * kStreamStages stages; after
+// the step loop the same memory holds each wave's O (16 heads x 128 dims F32
+// = 8 KiB) for the cross-wave reduction.
 template <typename QE, bool kFp8, int kSplit>
-__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_stream_kernel(DecodeArgs a) {
+__device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
   using Dec = StreamDecoder<QE, kFp8>;
   using vec8 = typename Dec::vec8;
-  constexpr int S = 2;  // pipeline stages (deeper pipelines measured no faster)
-  // S stages per wave; after the loop the same memory holds each wave's O
-  // (16 heads x 128 dims F32 = 8 KiB) for the cross-wave reduction.
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * S * Dec::kStageBytes];
-
-  const WorkItem item = schedule_item(a, blockIdx.x);
-  if (!item.valid) return;  // uniform across the workgroup
+  constexpr int S = kStreamStages;
   const uint32_t kvh = item.kvh;
   const uint32_t part = item.part;
   const uint32_t seq = item.seq;
@@ -1298,31 +1373,7 @@ void decode_stream_kernel(DecodeArgs a) {
   const uint32_t h = dec.c;
   const bool head_live = h < a.group;
   if (kSplit == 1) {
-    if (!head_live) return;
-    const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h;
-    if (a.parts == 1) {
-      const float inv = v_scale / l;
-      uint16_t* o = static_cast<uint16_t*>(a.output) + row * kDim + 4 * dec.g;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        uint32_t w0 = QE::from_f(dec.acc[dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][1] * inv)) << 16);
-        uint32_t w1 = QE::from_f(dec.acc[dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(o + dt * 16) = make_uint2(w0, w1);
-      }
-      if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m + log2f(l)) * kLn2;
-    } else {
-      const uint64_t state = row * a.parts + part;
-      float* o = a.ws_o + state * kDim + 4 * dec.g;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        *reinterpret_cast<float4*>(o + dt * 16) = make_float4(dec.acc[dt][0] * v_scale, dec.acc[dt][1] * v_scale,
-                                                             dec.acc[dt][2] * v_scale, dec.acc[dt][3] * v_scale);
-      }
-      if (dec.g == 0) {
-        a.ws_ml[state * 2] = dec.m;
-        a.ws_ml[state * 2 + 1] = l;
-      }
-    }
+    if (head_live) store_wave_result<QE>(a, dec, seq, kvh, part, v_scale, l);
     return;
   }
 
@@ -1357,13 +1408,23 @@ void decode_stream_kernel(DecodeArgs a) {
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
       const uint64_t state = row * a.parts + part;
-      a.ws_o[state * kDim + d] = O;
+      put_partial<QE>(a, state * kDim + d, O, 1.0f / L);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
         a.ws_ml[state * 2 + 1] = L;
       }
     }
   }
+}
+
+template <typename QE, bool kFp8, int kSplit>
+__global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_stream_kernel(DecodeArgs a) {
+  using Dec = StreamDecoder<QE, kFp8>;
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * kStreamStages * Dec::kStageBytes];
+  const WorkItem item = schedule_item(a, blockIdx.x);
+  if (!item.valid) return;  // uniform across the workgroup
+  stream_item<QE, kFp8, kSplit>(a, tiles, item);
 }
 
 // ---------------------------------------------------------------------------
@@ -1389,8 +1450,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
   const uint32_t n = min(min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts), kParts);
   const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
-  const float* os = a.ws_o + static_cast<uint64_t>(row) * a.parts * a.value_head_size;
+  using PT = typename PartialOut<QE>::T;
   const uint32_t Dv = a.value_head_size;
+  const uint32_t ps = partial_stride<QE>(Dv);
+  const PT* os = static_cast<const PT*>(a.ws_o) + static_cast<uint64_t>(row) * a.parts * ps;
   QT* out = static_cast<QT*>(a.output) + static_cast<uint64_t>(row) * Dv;
 
   const float mp = lane < n ? ml[2 * lane] : -INFINITY;
@@ -1400,9 +1463,17 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
     float v0[kParts], v1[kParts];
 #pragma unroll
     for (uint32_t j = 0; j < kParts; ++j) {
-      const float* src = os + static_cast<uint64_t>(j) * Dv + d;
-      v0[j] = j < n && d < Dv ? src[0] : 0.0f;
-      v1[j] = j < n && d + 1 < Dv ? src[1] : 0.0f;
+      const PT* src = os + static_cast<uint64_t>(j) * ps + d;
+      if constexpr (PartialOut<QE>::kNormalised) {
+        // Both dims in one aligned 4-byte word (the row stride is even; the
+        // padding element past an odd Dv is never used).
+        const uint32_t w = j < n && d < Dv ? *reinterpret_cast<const uint32_t*>(src) : 0U;
+        v0[j] = QE::to_f(static_cast<uint16_t>(w & 0xFFFFU));
+        v1[j] = QE::to_f(static_cast<uint16_t>(w >> 16));
+      } else {
+        v0[j] = j < n && d < Dv ? src[0] : 0.0f;
+        v1[j] = j < n && d + 1 < Dv ? src[1] : 0.0f;
+      }
     }
     float M = mp;
 #pragma unroll
@@ -1412,10 +1483,12 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
     float L = lp * f;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+    // Weight of partition p's stored output: f_p for sums, f_p l_p for normalised outputs.
+    const float wgt = PartialOut<QE>::kNormalised ? f * lp : f;
     float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
     for (uint32_t j = 0; j < kParts; ++j) {
-      const float fj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), j));
+      const float fj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
       o0 = fmaf(v0[j], fj, o0);
       o1 = fmaf(v1[j], fj, o1);
     }
@@ -1449,7 +1522,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
   const uint32_t n = (len + a.partition_tokens - 1) / a.partition_tokens;
   const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
-  const float* os = a.ws_o + static_cast<uint64_t>(row) * a.parts * a.value_head_size;
+  using PT = typename PartialOut<QE>::T;
+  const uint32_t ps = partial_stride<QE>(a.value_head_size);
+  const PT* os = static_cast<const PT*>(a.ws_o) + static_cast<uint64_t>(row) * a.parts * ps;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63U;
   const uint32_t wave = tid >> 6;
@@ -1478,23 +1553,40 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
 
   const uint32_t Dv = a.value_head_size;
   for (uint32_t d0 = 0; d0 < Dv; d0 += kMergeDimsPerPass) {
-    const uint32_t d_a = d0 + lane, d_b = d0 + 64 + lane;
+    // F32 partials: dims lane and 64 + lane; 16-bit partials: the pair 2 lane,
+    // 2 lane + 1, read as one aligned 4-byte word.
+    const uint32_t d_a = PartialOut<QE>::kNormalised ? d0 + 2 * lane : d0 + lane;
+    const uint32_t d_b = PartialOut<QE>::kNormalised ? d_a + 1 : d0 + 64 + lane;
+    auto pair = [&](const PT* o, float& va, float& vb) {
+      if constexpr (PartialOut<QE>::kNormalised) {
+        const uint32_t w = d_a < Dv ? *reinterpret_cast<const uint32_t*>(o + d_a) : 0U;
+        va = QE::to_f(static_cast<uint16_t>(w & 0xFFFFU));
+        vb = QE::to_f(static_cast<uint16_t>(w >> 16));
+      } else {
+        va = d_a < Dv ? o[d_a] : 0.0f;
+        vb = d_b < Dv ? o[d_b] : 0.0f;
+      }
+    };
     float acc_a = 0.0f, acc_b = 0.0f;
     for (uint32_t w0 = 0; w0 < n; w0 += kMergeWindow) {
       const uint32_t wn = min(kMergeWindow, n - w0);
       __syncthreads();
-      for (uint32_t p = tid; p < wn; p += kMergeThreads) factor[p] = exp2f(ml[2 * (w0 + p)] - M);
+      for (uint32_t p = tid; p < wn; p += kMergeThreads) {
+        const float f = exp2f(ml[2 * (w0 + p)] - M);
+        factor[p] = PartialOut<QE>::kNormalised ? f * ml[2 * (w0 + p) + 1] : f;  // weight of the stored output
+      }
       __syncthreads();
       uint32_t p = wave;
       for (; p + 3 * kMergeWaves < wn; p += 4 * kMergeWaves) {
-        const float* o0 = os + static_cast<uint64_t>(w0 + p) * Dv;
-        const float* o1 = o0 + kMergeWaves * static_cast<uint64_t>(Dv);
-        const float* o2 = o1 + kMergeWaves * static_cast<uint64_t>(Dv);
-        const float* o3 = o2 + kMergeWaves * static_cast<uint64_t>(Dv);
-        const float a0 = d_a < Dv ? o0[d_a] : 0.0f, b0 = d_b < Dv ? o0[d_b] : 0.0f;
-        const float a1 = d_a < Dv ? o1[d_a] : 0.0f, b1 = d_b < Dv ? o1[d_b] : 0.0f;
-        const float a2 = d_a < Dv ? o2[d_a] : 0.0f, b2 = d_b < Dv ? o2[d_b] : 0.0f;
-        const float a3 = d_a < Dv ? o3[d_a] : 0.0f, b3 = d_b < Dv ? o3[d_b] : 0.0f;
+        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * ps;
+        const PT* o1 = o0 + kMergeWaves * static_cast<uint64_t>(ps);
+        const PT* o2 = o1 + kMergeWaves * static_cast<uint64_t>(ps);
+        const PT* o3 = o2 + kMergeWaves * static_cast<uint64_t>(ps);
+        float a0, b0, a1, b1, a2, b2, a3, b3;
+        pair(o0, a0, b0);
+        pair(o1, a1, b1);
+        pair(o2, a2, b2);
+        pair(o3, a3, b3);
         const float f0 = factor[p], f1 = factor[p + kMergeWaves];
         const float f2 = factor[p + 2 * kMergeWaves], f3 = factor[p + 3 * kMergeWaves];
         acc_a = fmaf(a0, f0, acc_a);
@@ -1507,13 +1599,15 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
         acc_b = fmaf(b3, f3, acc_b);
       }
       for (; p < wn; p += kMergeWaves) {
-        const float* o0 = os + static_cast<uint64_t>(w0 + p) * Dv;
-        if (d_a < Dv) acc_a = fmaf(o0[d_a], factor[p], acc_a);
-        if (d_b < Dv) acc_b = fmaf(o0[d_b], factor[p], acc_b);
+        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * ps;
+        float a0, b0;
+        pair(o0, a0, b0);
+        acc_a = fmaf(a0, factor[p], acc_a);
+        acc_b = fmaf(b0, factor[p], acc_b);
       }
     }
-    part[wave][lane] = acc_a;
-    part[wave][64 + lane] = acc_b;
+    part[wave][d_a - d0] = acc_a;
+    part[wave][d_b - d0] = acc_b;
     __syncthreads();
     if (tid < kMergeDimsPerPass && d0 + tid < Dv) {
       float O = 0.0f;
@@ -1810,6 +1904,7 @@ bool stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   const uint64_t limit = 1ULL << 31;
   return 15 * p.k_page * es + 256 < limit && 15 * p.v_page * es + 256 < limit;
 }
+
 
 template <typename QE, typename CE>
 int launch_vector(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
