@@ -196,16 +196,83 @@ __device__ __forceinline__ void put_partial4(const DecodeArgs& a, uint64_t idx, 
 // ---------------------------------------------------------------------------
 // General kernel: any head size, dtype, stride and group size.
 // grid.x = parts * grid_y * sequences, grid_y = kv_heads * head_chunks *
-// value_tiles; 256 threads (4 waves). Each wave walks every fourth token of
-// the partition; per token the lanes split the head dimension and reduce.
+// value_tiles; 256 threads (4 waves). Each wave takes 64-token tiles of the
+// partition in turn (wave w: tiles w, w + 4, ...). Within a tile
+//   QK: lane i owns token i of the tile and forms its dot products with every
+//       query head of the workgroup (query staged in LDS), so a tile costs
+//       two wave reductions per head instead of one per token;
+//   PV: the lanes split the value dims and walk the tile's tokens, taking
+//       each token's probabilities and V row offset from its lane with
+//       readlane; the V loads of a step are independent.
+// The 64 block-table and K loads of a tile are all in flight together, so
+// short sequences are not a chain of dependent loads.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kVecThreads = 256;
 constexpr uint32_t kVecWaves = kVecThreads / 64;
 constexpr uint32_t kVecHeads = 8;      // query heads per workgroup
-constexpr uint32_t kVecDvTile = 256;   // value dims per workgroup
-constexpr uint32_t kVecDvPerLane = kVecDvTile / 64;
+constexpr uint32_t kVecQLds = 512;     // largest head size staged in LDS
 
-template <typename QE, typename CE>
+// Value dims per lane (1, 2 or 4; a workgroup covers 64 * kDvl of them) and
+// the V rows each PV step loads before its FMAs.
+__host__ __device__ constexpr uint32_t vec_pv_unroll(uint32_t dvl) { return 64 / dvl; }
+
+__host__ __device__ constexpr uint32_t vec_dims_per_lane(uint32_t dv) { return dv <= 64 ? 1 : dv <= 128 ? 2 : 4; }
+
+// Wave-wide reductions on DPP lane moves: quad swaps (xor 1, xor 2), the
+// 8-lane and 16-lane mirrors, then the four 16-lane row results combined
+// through scalar registers. Every lane gets the same value. (An xor-shuffle
+// butterfly compiles to ds_bpermute, an LDS round trip per step.)
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowMirror = 0x140;   // lane 15 - i within each 16-lane row
+constexpr int kDppHalfMirror = 0x141;  // lane 7 - i within each 8-lane half row
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_move<kDppQuadXor1>(v);
+  v += dpp_move<kDppQuadXor2>(v);
+  v += dpp_move<kDppHalfMirror>(v);
+  v += dpp_move<kDppRowMirror>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_move<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_move<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_move<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_move<kDppRowMirror>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
+// 16 bytes of cache elements as floats.
+template <typename CE>
+__device__ __forceinline__ void load16_as_float(const typename CE::T* src,
+                                                float (&out)[16 / sizeof(typename CE::T)]) {
+  using CT = typename CE::T;
+  constexpr uint32_t kW = 16 / sizeof(CT);
+  union {
+    uint4 u;
+    CT e[kW];
+  } w;
+  w.u = *reinterpret_cast<const uint4*>(src);
+#pragma unroll
+  for (uint32_t i = 0; i < kW; ++i) out[i] = CE::to_f(w.e[i]);
+}
+
+// kVecK: K rows are read as 16-byte vectors (head size, K strides and the
+// cache base all 16-byte aligned). kDvl: value dims per lane. kQLds: the
+// query is staged in LDS (head size <= kVecQLds), zero-padded to whole
+// 32-element chunks; otherwise it is read from global memory (uniform
+// addresses) at every use. kH: query heads per workgroup as compiled (1, 2,
+// 4 or 8; the group's own count may be smaller, the rest are zero rows).
+template <typename QE, typename CE, bool kVecK, uint32_t kDvl, bool kQLds, uint32_t kH>
 __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a) {
   using QT = typename QE::T;
   using CT = typename CE::T;
@@ -214,7 +281,10 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
   const uint32_t rest = bid / a.parts;
   uint32_t y = rest % a.grid_y;
   const uint32_t seq = rest / a.grid_y;
-  const uint32_t n_dvt = (a.value_head_size + kVecDvTile - 1) / kVecDvTile;
+  constexpr uint32_t kDvTile = 64 * kDvl;
+  constexpr uint32_t kUnroll = vec_pv_unroll(kDvl);
+  constexpr uint32_t kCh = 32;  // K elements per QK chunk
+  const uint32_t n_dvt = (a.value_head_size + kDvTile - 1) / kDvTile;
   const uint32_t dvt = y % n_dvt;
   y /= n_dvt;
   const uint32_t n_hc = (a.group + kVecHeads - 1) / kVecHeads;
@@ -226,12 +296,13 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
   if (p0 >= len) return;  // uniform: no partition state is produced
   const uint32_t p1 = min(p0 + a.partition_tokens, len);
 
-  const uint32_t heads = min(kVecHeads, a.group - hc * kVecHeads);
+  const uint32_t heads = min(kVecHeads, a.group - hc * kVecHeads);  // <= kH
   const uint32_t qh0 = kvh * a.group + hc * kVecHeads;
   const uint32_t lane = threadIdx.x & 63U;
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t D = a.head_size;
   const uint32_t Dv = a.value_head_size;
+  const uint32_t Dp = (D + kCh - 1) / kCh * kCh;  // LDS query row pitch
 
   float k_scale = 1.0f, v_scale = 1.0f;
   if (a.key_scales != nullptr) {
@@ -246,72 +317,182 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
   const CT* vc = static_cast<const CT*>(a.value_cache);
   const int32_t* table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
 
-  float m[kVecHeads], l[kVecHeads], o[kVecHeads][kVecDvPerLane];
+  // Block-table entry of this lane's token in the tile at t0; lanes past the
+  // end of the partition repeat token t0.
+  auto table_entry = [&](uint32_t t0) -> int32_t {
+    const uint32_t t = t0 + lane;
+    return table[(t < p1 ? t : t0) / a.block_size];
+  };
+  uint32_t t0 = p0 + wave * 64;
+  int32_t next_blk = t0 < p1 ? table_entry(t0) : 0;  // in flight during the query staging
+
+  __shared__ float sm_q[kQLds ? kVecHeads * kVecQLds : 1];
+  if constexpr (kQLds) {
+    for (uint32_t i = threadIdx.x; i < kH * Dp; i += kVecThreads) {
+      const uint32_t h = i / Dp, d = i % Dp;
+      sm_q[i] = h < heads && d < D ? QE::to_f(q[h * D + d]) : 0.0f;
+    }
+    __syncthreads();
+  }
+  auto qf = [&](uint32_t h, uint32_t d) -> float {
+    if constexpr (kQLds) {
+      return sm_q[h * Dp + d];
+    } else {
+      return h < heads && d < D ? QE::to_f(q[h * D + d]) : 0.0f;
+    }
+  };
+
+  float m[kH], l[kH], o[kH][kDvl];
 #pragma unroll
-  for (uint32_t h = 0; h < kVecHeads; ++h) {
+  for (uint32_t h = 0; h < kH; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.0f;
 #pragma unroll
-    for (uint32_t j = 0; j < kVecDvPerLane; ++j) o[h][j] = 0.0f;
+    for (uint32_t j = 0; j < kDvl; ++j) o[h][j] = 0.0f;
   }
 
-  for (uint32_t t = p0 + wave; t < p1; t += kVecWaves) {
-    const uint32_t page = t % a.block_size;
-    const uint64_t blk = static_cast<uint64_t>(table[t / a.block_size]);
+  for (; t0 < p1; t0 += kVecWaves * 64) {
+    // ---- QK: this lane's token -----------------------------------------
+    const uint32_t t = t0 + lane;
+    const bool valid = t < p1;
+    const uint32_t tc = valid ? t : t0;  // lanes past the end repeat token t0
+    const uint64_t blk = static_cast<uint64_t>(next_blk);
+    const uint32_t page = tc % a.block_size;
+    if (t0 + kVecWaves * 64 < p1) next_blk = table_entry(t0 + kVecWaves * 64);
     const uint64_t krow = blk * a.k_block + page * a.k_page + kvh * a.k_head;
     const uint64_t vrow = blk * a.v_block + page * a.v_page + kvh * a.v_head;
-    float acc[kVecHeads];
+    const uint32_t vrow_lo = static_cast<uint32_t>(vrow);
+    const uint32_t vrow_hi = static_cast<uint32_t>(vrow >> 32);
+    // V rows of tokens [i0, i0 + kUnroll) of the tile, lanes over value dims;
+    // token u's row offset comes from lane u (rows past the end of the tile
+    // repeat token t0). The first step is issued with the K loads below.
+    float vv[kUnroll][kDvl];
+    auto load_v = [&](uint32_t i0) {
 #pragma unroll
-    for (uint32_t h = 0; h < kVecHeads; ++h) acc[h] = 0.0f;
-    for (uint32_t d = lane; d < D; d += 64) {
-      const float kv = CE::to_f(kc[krow + d]);
+      for (uint32_t u = 0; u < kUnroll; ++u) {
+        const uint64_t row =
+            (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(vrow_hi, i0 + u))) << 32) |
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(vrow_lo, i0 + u));
+        const CT* vr = vc + row + dvt * kDvTile + lane;
 #pragma unroll
-      for (uint32_t h = 0; h < kVecHeads; ++h) {
-        if (h < heads) acc[h] = fmaf(QE::to_f(q[h * D + d]), kv, acc[h]);
+        for (uint32_t j = 0; j < kDvl; ++j) {
+          const uint32_t d = dvt * kDvTile + j * 64 + lane;
+          vv[u][j] = d < Dv ? CE::to_f(vr[j * 64]) : 0.0f;
+        }
+      }
+    };
+    load_v(0);
+    float acc[kH];
+#pragma unroll
+    for (uint32_t h = 0; h < kH; ++h) acc[h] = 0.0f;
+    if constexpr (kVecK) {
+      // 32-element chunks of the K row as 16-byte loads, double-buffered:
+      // chunk c + 1 is in flight while chunk c meets the query. Elements past
+      // the head size load as zero and meet zero query padding.
+      constexpr uint32_t kW = 16 / sizeof(CT);
+      constexpr uint32_t kKU = kCh / kW;
+      float ka[kKU][kW], kb[kKU][kW];
+      auto load_chunk = [&](float (&buf)[kKU][kW], uint32_t d0) {
+#pragma unroll
+        for (uint32_t u = 0; u < kKU; ++u) {
+          if (d0 + u * kW < D) {
+            load16_as_float<CE>(kc + krow + d0 + u * kW, buf[u]);
+          } else {
+#pragma unroll
+            for (uint32_t w = 0; w < kW; ++w) buf[u][w] = 0.0f;
+          }
+        }
+      };
+      auto fma_chunk = [&](const float (&buf)[kKU][kW], uint32_t d0) {
+#pragma unroll
+        for (uint32_t u = 0; u < kKU; ++u) {
+#pragma unroll
+          for (uint32_t h = 0; h < kH; ++h) {
+#pragma unroll
+            for (uint32_t w = 0; w < kW; ++w) acc[h] = fmaf(qf(h, d0 + u * kW + w), buf[u][w], acc[h]);
+          }
+        }
+      };
+      load_chunk(ka, 0);
+      for (uint32_t d0 = 0; d0 < D; d0 += 2 * kCh) {
+        const bool second = d0 + kCh < D;  // uniform
+        if (second) load_chunk(kb, d0 + kCh);
+        fma_chunk(ka, d0);
+        if (!second) break;
+        if (d0 + 2 * kCh < D) load_chunk(ka, d0 + 2 * kCh);
+        fma_chunk(kb, d0 + kCh);
+      }
+    } else {
+#pragma unroll 8
+      for (uint32_t d = 0; d < D; ++d) {
+        const float kv = CE::to_f(kc[krow + d]);
+#pragma unroll
+        for (uint32_t h = 0; h < kH; ++h) acc[h] = fmaf(qf(h, d), kv, acc[h]);
       }
     }
-    float vv[kVecDvPerLane];
+
+    // ---- online softmax over the tile -----------------------------------
+    float alpha[kH], pv[kH];  // pv: v_scale * p of this lane's token
 #pragma unroll
-    for (uint32_t j = 0; j < kVecDvPerLane; ++j) {
-      const uint32_t d = dvt * kVecDvTile + j * 64 + lane;
-      vv[j] = d < Dv ? CE::to_f(vc[vrow + d]) * v_scale : 0.0f;
-    }
-#pragma unroll
-    for (uint32_t h = 0; h < kVecHeads; ++h) {
+    for (uint32_t h = 0; h < kH; ++h) {
+      alpha[h] = 1.0f;
+      pv[h] = 0.0f;
       if (h < heads) {
-        const float s = wave_sum(acc[h]) * sl2;
-        const float mn = fmaxf(m[h], s);
-        const float alpha = exp2f(m[h] - mn);
-        const float p = exp2f(s - mn);
-        l[h] = fmaf(l[h], alpha, p);
-#pragma unroll
-        for (uint32_t j = 0; j < kVecDvPerLane; ++j) o[h][j] = fmaf(o[h][j], alpha, p * vv[j]);
+        const float s = valid ? acc[h] * sl2 : -INFINITY;
+        const float mn = fmaxf(m[h], wave_max_dpp(s));
+        alpha[h] = exp2f(m[h] - mn);
+        const float pr = valid ? exp2f(s - mn) : 0.0f;
+        l[h] = fmaf(l[h], alpha[h], wave_sum_dpp(pr));
         m[h] = mn;
+        pv[h] = pr * v_scale;
+      }
+    }
+
+    // ---- PV: lanes over value dims, tokens of the tile in turn -------------
+    // Token u's probabilities come from lane u by readlane (scalar operands,
+    // no LDS round trip); past the end of the tile, and for absent heads,
+    // they are zero.
+#pragma unroll
+    for (uint32_t h = 0; h < kH; ++h) {
+#pragma unroll
+      for (uint32_t j = 0; j < kDvl; ++j) o[h][j] *= alpha[h];
+    }
+    const uint32_t ntok = min(64U, p1 - t0);
+    for (uint32_t i0 = 0; i0 < ntok; i0 += kUnroll) {
+      if (i0 != 0) load_v(i0);
+#pragma unroll
+      for (uint32_t u = 0; u < kUnroll; ++u) {
+#pragma unroll
+        for (uint32_t h = 0; h < kH; ++h) {
+          const float pr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv[h]), i0 + u));
+#pragma unroll
+          for (uint32_t j = 0; j < kDvl; ++j) o[h][j] = fmaf(pr, vv[u][j], o[h][j]);
+        }
       }
     }
   }
 
-  __shared__ float sm_m[kVecWaves][kVecHeads];
-  __shared__ float sm_l[kVecWaves][kVecHeads];
-  __shared__ float sm_o[kVecWaves][kVecHeads][kVecDvTile];
+  __shared__ float sm_m[kVecWaves][kH];
+  __shared__ float sm_l[kVecWaves][kH];
+  __shared__ float sm_o[kVecWaves][kH][kDvTile];
   if (lane == 0) {
 #pragma unroll
-    for (uint32_t h = 0; h < kVecHeads; ++h) {
+    for (uint32_t h = 0; h < kH; ++h) {
       sm_m[wave][h] = m[h];
       sm_l[wave][h] = l[h];
     }
   }
 #pragma unroll
-  for (uint32_t h = 0; h < kVecHeads; ++h) {
+  for (uint32_t h = 0; h < kH; ++h) {
 #pragma unroll
-    for (uint32_t j = 0; j < kVecDvPerLane; ++j) sm_o[wave][h][j * 64 + lane] = o[h][j];
+    for (uint32_t j = 0; j < kDvl; ++j) sm_o[wave][h][j * 64 + lane] = o[h][j];
   }
   __syncthreads();
 
-  for (uint32_t idx = threadIdx.x; idx < kVecHeads * kVecDvTile; idx += kVecThreads) {
-    const uint32_t h = idx / kVecDvTile;
-    const uint32_t dd = idx % kVecDvTile;
-    const uint32_t d = dvt * kVecDvTile + dd;
+  for (uint32_t idx = threadIdx.x; idx < kH * kDvTile; idx += kVecThreads) {
+    const uint32_t h = idx / kDvTile;
+    const uint32_t dd = idx % kDvTile;
+    const uint32_t d = dvt * kDvTile + dd;
     if (h >= heads || d >= Dv) continue;
     float M = -INFINITY;
 #pragma unroll
@@ -1906,12 +2087,57 @@ bool stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
 }
 
 
-template <typename QE, typename CE>
-int launch_vector(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
+template <typename QE, typename CE, bool kVecK, uint32_t kDvl, bool kQLds, uint32_t kH>
+int launch_vector_kernel(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  hipLaunchKernelGGL((decode_vector_kernel<QE, CE>), dim3(static_cast<uint32_t>(grid)),
+  hipLaunchKernelGGL((decode_vector_kernel<QE, CE, kVecK, kDvl, kQLds, kH>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kVecThreads), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
+// 16-byte K vectors need the head size, every K stride and the cache base to
+// be multiples of 16 bytes.
+template <typename CE>
+bool vector_k_aligned(const DecodeArgs& args) {
+  constexpr uint64_t kW = 16 / sizeof(typename CE::T);
+  return args.head_size % kW == 0 && args.k_block % kW == 0 && args.k_page % kW == 0 &&
+         args.k_head % kW == 0 && reinterpret_cast<uintptr_t>(args.key_cache) % 16 == 0;
+}
+
+// The general kernel's common path: 16-byte K vectors and the query in LDS.
+// It is compiled per value dims per lane (sized to Dv) and per heads class;
+// every other shape takes 256-dim value tiles and 8-head workgroups.
+template <typename CE>
+bool vector_common_path(const DecodeArgs& args) {
+  return vector_k_aligned<CE>(args) && args.head_size <= kVecQLds;
+}
+
+template <typename CE>
+uint32_t vector_dims_per_lane(const DecodeArgs& args) {
+  return vector_common_path<CE>(args) ? vec_dims_per_lane(args.value_head_size) : 4;
+}
+
+template <typename QE, typename CE, uint32_t kDvl>
+int launch_vector_heads(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
+  const uint32_t g = args.group < kVecHeads ? args.group : kVecHeads;
+  if (g == 1) return launch_vector_kernel<QE, CE, true, kDvl, true, 1>(args, grid, stream);
+  if (g == 2) return launch_vector_kernel<QE, CE, true, kDvl, true, 2>(args, grid, stream);
+  if (g <= 4) return launch_vector_kernel<QE, CE, true, kDvl, true, 4>(args, grid, stream);
+  return launch_vector_kernel<QE, CE, true, kDvl, true, 8>(args, grid, stream);
+}
+
+template <typename QE, typename CE>
+int launch_vector(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
+  if (args.head_size > kVecQLds) {
+    return vector_k_aligned<CE>(args) ? launch_vector_kernel<QE, CE, true, 4, false, 8>(args, grid, stream)
+                                      : launch_vector_kernel<QE, CE, false, 4, false, 8>(args, grid, stream);
+  }
+  if (!vector_k_aligned<CE>(args)) return launch_vector_kernel<QE, CE, false, 4, true, 8>(args, grid, stream);
+  switch (vector_dims_per_lane<CE>(args)) {
+    case 1: return launch_vector_heads<QE, CE, 1>(args, grid, stream);
+    case 2: return launch_vector_heads<QE, CE, 2>(args, grid, stream);
+    default: return launch_vector_heads<QE, CE, 4>(args, grid, stream);
+  }
 }
 
 template <typename QE>
@@ -1986,7 +2212,8 @@ int run_typed(const Problem& p, hipStream_t stream) {
     }
   } else {
     const uint64_t n_hc = (group + kVecHeads - 1) / kVecHeads;
-    const uint64_t n_dvt = (p.value_head_size + kVecDvTile - 1) / kVecDvTile;
+    const uint64_t dv_tile = 64ULL * (fp8 ? vector_dims_per_lane<Fp8Elem>(args) : vector_dims_per_lane<QE>(args));
+    const uint64_t n_dvt = (p.value_head_size + dv_tile - 1) / dv_tile;
     const uint64_t gy = static_cast<uint64_t>(p.kv_heads) * n_hc * n_dvt;
     const uint64_t grid = parts * gy * p.sequences;
     if (gy > std::numeric_limits<uint32_t>::max() ||
@@ -2039,11 +2266,12 @@ uint32_t split_k_partition_tokens(uint32_t sequences, uint32_t query_heads, uint
       value_head_size == 0 || max_sequence_length == 0 || query_heads % kv_heads != 0)
     return 0;
   const uint64_t work = static_cast<uint64_t>(sequences) * kv_heads;
-  if (work >= 1024 || max_sequence_length < 1024) return 0;
+  if (work >= 1024 || max_sequence_length < 512) return 0;
   const uint64_t want_parts = (2048 + work - 1) / work;
   uint64_t tokens = (max_sequence_length + want_parts - 1) / want_parts;
   tokens = ((tokens + kChunk - 1) / kChunk) * kChunk;
-  if (tokens < 512) tokens = 512;
+  const uint64_t floor_tokens = work < 256 ? 64 : 512;
+  if (tokens < floor_tokens) tokens = floor_tokens;
   if (parts_for(max_sequence_length, static_cast<uint32_t>(tokens)) < 2) return 0;
   return static_cast<uint32_t>(tokens);
 }

@@ -46,6 +46,9 @@ CASES = [
     (2, 16, 2, 128, 128, 16, [3000, 1]),
     (2, 4, 1, 128, 128, 1, [70, 33]),
     (2, 32, 1, 128, 128, 16, [1500, 77]),
+    # general kernel: two 256-dim value tiles; a head size past the query's LDS stage
+    (2, 8, 2, 64, 320, 16, [100, 300]),
+    (2, 4, 2, 640, 64, 16, [70, 150]),
 ]
 
 
