@@ -1608,6 +1608,25 @@ void decode_stream_kernel(DecodeArgs a) {
   stream_item<QE, kFp8, kSplit>(a, tiles, item);
 }
 
+// kGroup consecutive work items per workgroup, one wave each and independent
+// (the single-wave path has no workgroup barrier). With the KV head varying
+// fastest in the schedule, a workgroup holds adjacent heads of one
+// (sequence, partition): their rows of each block share pages and are
+// requested from one CU at about the same time, which the memory system
+// serves faster than the same rows requested from CUs on different XCDs.
+constexpr int kStreamGroup = 4;
+
+template <typename QE, bool kFp8, int kGroup>
+__global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_stream_group_kernel(DecodeArgs a) {
+  using Dec = StreamDecoder<QE, kFp8>;
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * kStreamStages * Dec::kStageBytes];
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
+  if (!item.valid) return;  // per wave: nothing below waits on the other waves
+  stream_item<QE, kFp8, 1>(a, tiles + wave * kStreamStages * Dec::kStageBytes, item);
+}
+
 // ---------------------------------------------------------------------------
 // Split-K merge for at most kMergeRowParts partitions (the log-sum-exp
 // identity of paged_decode_attention.cu:780-852): one wave per (sequence,
@@ -2066,6 +2085,15 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
+template <typename QE, bool kFp8>
+int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
+  TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  const uint64_t groups = (items + kStreamGroup - 1) / kStreamGroup;
+  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kStreamGroup>), dim3(static_cast<uint32_t>(groups)),
+                     dim3(kStreamGroup * 64), 0, stream, args);
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
 template <typename QE, bool kFp8, int kSplit>
 int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
@@ -2198,7 +2226,7 @@ int run_typed(const Problem& p, hipStream_t stream) {
       // waves when that leaves at least 2 steps per wave. (16-wave groups
       // measured slower: they add no CUs, only contention within one.)
       if (grid >= 4096 || steps < 8) {
-        status = fp8 ? launch_stream<QE, true, 1>(args, grid, stream) : launch_stream<QE, false, 1>(args, grid, stream);
+        status = fp8 ? launch_stream_group<QE, true>(args, grid, stream) : launch_stream_group<QE, false>(args, grid, stream);
       } else {
         status = fp8 ? launch_stream<QE, true, 4>(args, grid, stream) : launch_stream<QE, false, 4>(args, grid, stream);
       }
