@@ -1820,6 +1820,87 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
 }
 
+// Split-K merge, latency path for the common shape: 16-bit partials, Dv = 128,
+// at most 256 partitions (partial rows of 256 bytes, 16-byte aligned). One
+// workgroup of 256 threads per row; thread (g, c) owns dims 8c..8c+7 of
+// partitions g, g + 16, ... All of a row's partial loads and its (m, l) loads
+// are issued at the start, so the row costs one memory round trip; the
+// weights w_p = 2^(m_p - M) l_p and L = sum w_p come from two block
+// reductions while the partials are in flight, and the 16 partition groups
+// are summed in LDS.
+constexpr uint32_t kMergeFastParts = 256;
+constexpr uint32_t kMergeFastDim = 128;
+
+template <typename QE>
+__global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs a) {
+  using QT = typename QE::T;
+  constexpr uint32_t kGroups = kMergeThreads / 16;            // partition groups
+  constexpr uint32_t kPerThread = kMergeFastParts / kGroups;  // partitions per thread
+  __shared__ float wgt[kMergeFastParts];
+  __shared__ float red[kMergeWaves];
+  __shared__ float part[kGroups][kMergeFastDim + 4];
+  const uint32_t row = blockIdx.x;
+  const uint32_t seq = row / a.query_heads;
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  const uint32_t n = min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts);  // <= 256
+  const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
+  const uint16_t* os = static_cast<const uint16_t*>(a.ws_o) + static_cast<uint64_t>(row) * a.parts * kMergeFastDim;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63U;
+  const uint32_t wave = tid >> 6;
+  const uint32_t c = tid & 15U;
+  const uint32_t g = tid >> 4;
+
+  uint4 ov[kPerThread];
+#pragma unroll
+  for (uint32_t i = 0; i < kPerThread; ++i) {
+    const uint32_t p = g + kGroups * i;
+    ov[i] = p < n ? *reinterpret_cast<const uint4*>(os + static_cast<uint64_t>(p) * kMergeFastDim + 8 * c)
+                  : make_uint4(0U, 0U, 0U, 0U);
+  }
+  const float m = tid < n ? ml[2 * tid] : -INFINITY;
+  const float lp = tid < n ? ml[2 * tid + 1] : 0.0f;
+
+  float M = wave_max_dpp(m);
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = red[0];
+#pragma unroll
+  for (uint32_t w = 1; w < kMergeWaves; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  const float w = tid < n ? exp2f(m - M) * lp : 0.0f;  // weight of the stored O_p / l_p
+  wgt[tid] = w;
+  const float ws = wave_sum_dpp(w);
+  if (lane == 0) red[wave] = ws;
+  __syncthreads();
+  float L = 0.0f;
+#pragma unroll
+  for (uint32_t v = 0; v < kMergeWaves; ++v) L += red[v];
+
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (uint32_t i = 0; i < kPerThread; ++i) {
+    const uint32_t p = g + kGroups * i;
+    const float f = p < n ? wgt[p] : 0.0f;
+    const uint32_t words[4] = {ov[i].x, ov[i].y, ov[i].z, ov[i].w};
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      acc[2 * j] = fmaf(QE::to_f(static_cast<uint16_t>(words[j] & 0xFFFFU)), f, acc[2 * j]);
+      acc[2 * j + 1] = fmaf(QE::to_f(static_cast<uint16_t>(words[j] >> 16)), f, acc[2 * j + 1]);
+    }
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < 8; ++j) part[g][8 * c + j] = acc[j];
+  __syncthreads();
+  if (tid < kMergeFastDim) {
+    float O = 0.0f;
+#pragma unroll
+    for (uint32_t v = 0; v < kGroups; ++v) O += part[v][tid];
+    static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * kMergeFastDim + tid] = QE::from_f(O / L);
+  }
+  if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
+}
+
 // ---------------------------------------------------------------------------
 // Host side: error reporting, telemetry, validation, planning, launch.
 // ---------------------------------------------------------------------------
@@ -2063,6 +2144,9 @@ int launch_merge(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
     hipLaunchKernelGGL((merge_kernel<QE, 16>), grid, dim3(kMergeThreads), 0, stream, args, rows);
   } else if (args.parts <= kMergeRowParts) {
     hipLaunchKernelGGL((merge_kernel<QE, kMergeRowParts>), grid, dim3(kMergeThreads), 0, stream, args, rows);
+  } else if (PartialOut<QE>::kNormalised && args.value_head_size == kMergeFastDim &&
+             args.parts <= kMergeFastParts && reinterpret_cast<uintptr_t>(args.ws_o) % 16 == 0) {
+    hipLaunchKernelGGL(merge_rows128_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
   } else {
     hipLaunchKernelGGL(merge_wide_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
   }
@@ -2221,12 +2305,16 @@ int run_typed(const Problem& p, hipStream_t stream) {
     const uint32_t chunks = (partition_tokens + kChunk - 1) / kChunk;
     const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
     if (stream_eligible(p, parts, group)) {
-      // Waves per workgroup: one when the grid alone fills the chip's 4096
-      // wave slots (16 per CU); otherwise each partition is split over 4
-      // waves when that leaves at least 2 steps per wave. (16-wave groups
+      // A grid that fills the chip's 4096 wave slots (16 per CU) runs one
+      // wave per item, four items (adjacent KV heads) per workgroup. Smaller
+      // grids split each partition over 4 waves when that leaves at least 2
+      // steps per wave, else run one wave per workgroup: there the number of
+      // CUs in use matters more than co-locating heads. (16-wave groups
       // measured slower: they add no CUs, only contention within one.)
-      if (grid >= 4096 || steps < 8) {
+      if (grid >= 4096) {
         status = fp8 ? launch_stream_group<QE, true>(args, grid, stream) : launch_stream_group<QE, false>(args, grid, stream);
+      } else if (steps < 8) {
+        status = fp8 ? launch_stream<QE, true, 1>(args, grid, stream) : launch_stream<QE, false, 1>(args, grid, stream);
       } else {
         status = fp8 ? launch_stream<QE, true, 4>(args, grid, stream) : launch_stream<QE, false, 4>(args, grid, stream);
       }

@@ -587,10 +587,10 @@ def main() -> int:
                                                                                           "decode_vector_kernel")
     if family == "mfma-stream":
         # the library's launch rule: grouped single-wave items when the grid fills the chip
-        # (>= 4096 work items) or partitions are short (< 8 steps of 16 tokens)
+        # (>= 4096 work items)
         pt = case.partition_tokens or case.max_sequence_length
         items = -(-case.max_sequence_length // pt) * case.kv_heads * case.sequences
-        if items >= 4096 or -(-pt // 16) < 8:
+        if items >= 4096:
             kernel_name = "decode_stream_group_kernel"
 
     cpu = None
