@@ -1125,17 +1125,27 @@ __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, u
 
 __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
 
+// Pipeline stages per wave: a 16-bit stage is 8 KiB of K/V rows, an FP8
+// stage 4 KiB. Deeper pipelines measured no faster for either (FP8 with 2, 3
+// and 4 stages ran C4 at the same speed).
+constexpr int kStreamStages = 2;
+constexpr int kStreamStagesFp8 = 2;
+
 template <typename QE, bool kFp8>
 struct StreamDecoder {
   static constexpr uint32_t kPitch = kTileRowBytes;  // bytes between consecutive tokens' rows in a stage
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
-  // Stage layout per wave. 16-bit: [K 4 KiB | V 4 KiB]. FP8: [K bytes 2 KiB |
-  // V bytes 2 KiB | V as 16 bits 4 KiB]. kVOff locates the 16-bit V tile.
-  static constexpr uint32_t kStageBytes = 2 * kStepTileBytes;
+  // LDS per wave. 16-bit: kStages stages of [K 4 KiB | V 4 KiB]; PV reads V
+  // in place. FP8: kStages stages of [K bytes 2 KiB | V bytes 2 KiB], then
+  // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
+  static constexpr int kStages = kFp8 ? kStreamStagesFp8 : kStreamStages;
   static constexpr uint32_t kF8TileBytes = kStep * kDim;  // 2 KiB
-  static constexpr uint32_t kVOff = kFp8 ? 2 * kF8TileBytes : kStepTileBytes;
+  static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kStepTileBytes;
+  static constexpr uint32_t kVOff = kStepTileBytes;  // 16-bit: V within a stage
+  static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
+  static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStepTileBytes : 0);
   static constexpr int kDmaPerStep = kFp8 ? 4 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
@@ -1243,13 +1253,13 @@ struct StreamDecoder {
     return z;
   }
 
-  // FP8 V bytes -> the swizzled 16-bit V tile: lane handles 32 bytes of token
-  // lane >> 2 (rows past the sequence end become zero).
-  __device__ __forceinline__ void stage_v_fp8(uint8_t* stage, uint32_t t0) const {
+  // FP8 V bytes of a stage -> the wave's swizzled 16-bit V tile: lane
+  // handles 32 bytes of token lane >> 2 (rows past the sequence end become
+  // zero).
+  __device__ __forceinline__ void stage_v_fp8(const uint8_t* stage, uint8_t* tile, uint32_t t0) const {
     const uint32_t t = lane >> 2;
     const bool live = t0 + t < len;
     const uint8_t* vrow = stage + kF8TileBytes + t * kDim;
-    uint8_t* tile = stage + kVOff;
     const uint32_t odd = lane & 1U;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -1431,22 +1441,23 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
   }
 }
 
-constexpr int kStreamStages = 2;  // pipeline stages (deeper pipelines measured no faster)
 
 // One work item of the streaming kernel, from its first loads to its
-// partial-state stores. `tiles` holds kSplit * kStreamStages stages; after
-// the step loop the same memory holds each wave's O (16 heads x 128 dims F32
-// = 8 KiB) for the cross-wave reduction.
+// partial-state stores. `tiles` holds kSplit waves' LDS (Dec::kWaveBytes
+// each); after the step loop the same memory holds each wave's O (16 heads x
+// 128 dims F32 = 8 KiB) for the cross-wave reduction.
 template <typename QE, bool kFp8, int kSplit>
 __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
   using Dec = StreamDecoder<QE, kFp8>;
   using vec8 = typename Dec::vec8;
-  constexpr int S = kStreamStages;
+  constexpr int S = Dec::kStages;
   const uint32_t kvh = item.kvh;
   const uint32_t part = item.part;
   const uint32_t seq = item.seq;
   const uint32_t len = item.len;
   const uint32_t p0 = part * a.partition_tokens;
+  static_assert(kSplit * Dec::kWaveBytes >= kSplit * 16 * kDim * sizeof(float),
+                "the cross-wave reduction reuses the stages");
 
   Dec dec(a);
   dec.lane = threadIdx.x & 63U;
@@ -1465,7 +1476,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   dec.vbase = reinterpret_cast<uint64_t>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head * es;
   dec.init_offsets();
   const uint32_t wave = kSplit == 1 ? 0U : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* tw = tiles + wave * S * Dec::kStageBytes;
+  uint8_t* tw = tiles + wave * Dec::kWaveBytes;
 
   float k_scale = 1.0f, v_scale = 1.0f;
   if (kFp8) {
@@ -1527,11 +1538,11 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
         if (n + i < my_n) {
           const uint32_t t0 = t_first + (n + i) * st;
           const uint32_t tn = min(t0 + S * st, t_last);
-          uint8_t* vtile = tl[i] + Dec::kVOff;
+          uint8_t* vtile = kFp8 ? tw + Dec::kVTileOff : tl[i] + Dec::kVOff;
           vm_wait_dma<Dec::kDmaPerStep * (S - 1)>();  // this step's loads; S - 1 steps stay in flight
           scalar_ready(nx[i]);
           if (kFp8) {
-            dec.stage_v_fp8(tl[i], t0);
+            dec.stage_v_fp8(tl[i], vtile, t0);
           } else {
             dec.zero_dead_rows(vtile, t0);
           }
@@ -1602,7 +1613,7 @@ template <typename QE, bool kFp8, int kSplit>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8>;
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * kStreamStages * Dec::kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * Dec::kWaveBytes];
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
   stream_item<QE, kFp8, kSplit>(a, tiles, item);
@@ -1620,11 +1631,11 @@ template <typename QE, bool kFp8, int kGroup>
 __global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_group_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8>;
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * kStreamStages * Dec::kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * Dec::kWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
   if (!item.valid) return;  // per wave: nothing below waits on the other waves
-  stream_item<QE, kFp8, 1>(a, tiles + wave * kStreamStages * Dec::kStageBytes, item);
+  stream_item<QE, kFp8, 1>(a, tiles + wave * Dec::kWaveBytes, item);
 }
 
 // ---------------------------------------------------------------------------
