@@ -1126,12 +1126,15 @@ __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, u
 __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
 
 // Pipeline stages per wave: a 16-bit stage is 8 KiB of K/V rows, an FP8
-// stage 4 KiB. Deeper pipelines measured no faster for either (FP8 with 2, 3
-// and 4 stages ran C4 at the same speed).
+// stage 4 KiB. Deeper pipelines measured no faster (FP8 with 2, 3 and 4
+// stages ran C4 at the same speed; two head tiles per wave ran C5 slower
+// with 4 and 6 stages than with 2).
 constexpr int kStreamStages = 2;
 constexpr int kStreamStagesFp8 = 2;
 
-template <typename QE, bool kFp8>
+// kHT: 16-query-head tiles per wave (1, or 2 for groups of 17-32 heads). The
+// tiles share each step's K operand fetches and V transposed reads.
+template <typename QE, bool kFp8, int kHT = 1>
 struct StreamDecoder {
   static constexpr uint32_t kPitch = kTileRowBytes;  // bytes between consecutive tokens' rows in a stage
   using Ops = MfmaOps<QE>;
@@ -1162,10 +1165,10 @@ struct StreamDecoder {
   uint32_t f8_k_voff[2], f8_v_voff[2];  // FP8: lane's K / V DMA offsets, rows 8i .. 8i + 7
   float sl2;
 
-  vec8 qb[4];
-  f32x4 acc[8];  // O^T: dims dt*16 + 4g + r, head c
-  float m;       // running max (log2 units) of head c
-  float lsum;    // partial denominator over this lane's tokens
+  vec8 qb[kHT][4];
+  f32x4 acc[kHT][8];  // O^T of tile ht: dims dt*16 + 4g + r, head 16 ht + c
+  float m[kHT];       // running max (log2 units) of head 16 ht + c
+  float lsum[kHT];    // partial denominator over this lane's tokens
 
   __device__ __forceinline__ StreamDecoder(const DecodeArgs& args) : a(args) {}
 
@@ -1243,14 +1246,16 @@ struct StreamDecoder {
     }
   }
 
-  __device__ __forceinline__ f32x4 qk(const uint8_t* stage) const {
-    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+  __device__ __forceinline__ void qk(const uint8_t* stage, f32x4 (&z)[kHT]) const {
     vec8 kop[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) kop[kc] = k_operand(stage, kc);
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) z = Ops::mma(kop[kc], qb[kc], z);
-    return z;
+    for (int ht = 0; ht < kHT; ++ht) {
+      z[ht] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) z[ht] = Ops::mma(kop[kc], qb[ht][kc], z[ht]);
+    }
   }
 
   // FP8 V bytes of a stage -> the wave's swizzled 16-bit V tile: lane
@@ -1287,41 +1292,46 @@ struct StreamDecoder {
     }
   }
 
-  __device__ __forceinline__ void softmax_pv(f32x4 s, uint32_t t0, const uint8_t* tile) {
-    float cmax = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = t0 + 4 * g + r < p1 ? s[r] * sl2 : -INFINITY;
-      s[r] = v;
-      cmax = fmaxf(cmax, v);
-    }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-    const float mn = fmaxf(m, cmax);  // finite: every step has a valid token
-    // Rescale only when some head's maximum moved (exact; usually skipped).
-    if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);
-      lsum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-      m = mn;
-    }
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(s[r] - m);
-      lsum += p[r];
-    }
-    const uint32_t w0 = Ops::pack2(p[0], p[1]), w1 = Ops::pack2(p[2], p[3]);
+  __device__ __forceinline__ void softmax_pv(f32x4 (&s)[kHT], uint32_t t0, const uint8_t* tile) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const vec4 pb = __builtin_bit_cast(vec4, u32x2{w0, w1});
+    vec4 pb[kHT];
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = t0 + 4 * g + r < p1 ? s[ht][r] * sl2 : -INFINITY;
+        s[ht][r] = v;
+        cmax = fmaxf(cmax, v);
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      const float mn = fmaxf(m[ht], cmax);  // finite: every step has a valid token
+      // Rescale only when some head's maximum moved (exact; usually skipped).
+      if (__builtin_amdgcn_ballot_w64(mn > m[ht]) != 0) {
+        const float alpha = __builtin_amdgcn_exp2f(m[ht] - mn);
+        lsum[ht] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[ht][dt] *= alpha;
+        m[ht] = mn;
+      }
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(s[ht][r] - m[ht]);
+        lsum[ht] += p[r];
+      }
+      const uint32_t w0 = Ops::pack2(p[0], p[1]), w1 = Ops::pack2(p[2], p[3]);
+      pb[ht] = __builtin_bit_cast(vec4, u32x2{w0, w1});
+    }
     const uint32_t k = c >> 2, q = c & 3U;
     lds_u8* base = (lds_u8*)tile;
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; ++dt) {
       const uint32_t off = vtile_off<kPitch>(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
       const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
-      acc[dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb, acc[dt]);
+#pragma unroll
+      for (int ht = 0; ht < kHT; ++ht) acc[ht][dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb[ht], acc[ht][dt]);
     }
   }
 };
@@ -1416,26 +1426,26 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
 // partial output (PartialOut encoding) and (m, l) in the split-K workspace. Lane (g, c) holds dims
 // dt*16 + 4g .. +3 of head c; only lanes of live heads call this.
 template <typename QE, typename Dec>
-__device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec& dec, uint32_t seq, uint32_t kvh,
-                                                  uint32_t part, float v_scale, float l) {
-  const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + dec.c;
+__device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec& dec, int ht, uint32_t seq,
+                                                  uint32_t head0, uint32_t part, float v_scale, float l) {
+  const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + head0 + dec.c;
   if (a.parts == 1) {
     const float inv = v_scale / l;
     uint16_t* o = static_cast<uint16_t*>(a.output) + row * kDim + 4 * dec.g;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      uint32_t w0 = QE::from_f(dec.acc[dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][1] * inv)) << 16);
-      uint32_t w1 = QE::from_f(dec.acc[dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[dt][3] * inv)) << 16);
+      uint32_t w0 = QE::from_f(dec.acc[ht][dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[ht][dt][1] * inv)) << 16);
+      uint32_t w1 = QE::from_f(dec.acc[ht][dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[ht][dt][3] * inv)) << 16);
       *reinterpret_cast<uint2*>(o + dt * 16) = make_uint2(w0, w1);
     }
-    if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m + log2f(l)) * kLn2;
+    if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m[ht] + log2f(l)) * kLn2;
   } else {
     const uint64_t state = row * a.parts + part;
     const float inv_l = 1.0f / l;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) put_partial4<QE>(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[dt], v_scale, inv_l);
+    for (int dt = 0; dt < 8; ++dt) put_partial4<QE>(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
     if (dec.g == 0) {
-      a.ws_ml[state * 2] = dec.m;
+      a.ws_ml[state * 2] = dec.m[ht];
       a.ws_ml[state * 2 + 1] = l;
     }
   }
@@ -1446,9 +1456,10 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
 // partial-state stores. `tiles` holds kSplit waves' LDS (Dec::kWaveBytes
 // each); after the step loop the same memory holds each wave's O (16 heads x
 // 128 dims F32 = 8 KiB) for the cross-wave reduction.
-template <typename QE, bool kFp8, int kSplit>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1>
 __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
-  using Dec = StreamDecoder<QE, kFp8>;
+  static_assert(kHT == 1 || kSplit == 1, "two head tiles run one wave per item");
+  using Dec = StreamDecoder<QE, kFp8, kHT>;
   using vec8 = typename Dec::vec8;
   constexpr int S = Dec::kStages;
   const uint32_t kvh = item.kvh;
@@ -1494,10 +1505,13 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   const uint32_t t_first = p0 + wave * kStep;
   const uint32_t t_last = t_first + (my_n > 0 ? my_n - 1 : 0) * st;
 
-  dec.m = -INFINITY;
-  dec.lsum = 0.0f;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) dec.acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int ht = 0; ht < kHT; ++ht) {
+    dec.m[ht] = -INFINITY;
+    dec.lsum[ht] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) dec.acc[ht][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
   if (my_n > 0) {
     // Block IDs run S steps ahead of the loads that use them.
@@ -1518,19 +1532,31 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     // Q is loaded after the first steps' K/V and waited for together with
     // them, so a wave's start costs one memory round trip, not two.
     {
-      const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
-                             (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + min(dec.c, a.group - 1U)) *
-                                 kDim;
-      u32x4 qw[4];
+      u32x4 qw[kHT][4];
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
-        vm_load16(qw[kc], qrow + dim);
+      for (int ht = 0; ht < kHT; ++ht) {
+        const uint32_t h = min(ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
+                               (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kDim;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
+          vm_load16(qw[ht][kc], qrow + dim);
+        }
       }
-      vm_wait_all(qw);
-      const bool live = dec.c < a.group;
+      vm_wait_all(qw[0]);
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) dec.qb[kc] = __builtin_bit_cast(vec8, live ? qw[kc] : u32x4{0U, 0U, 0U, 0U});
+      for (int ht = 1; ht < kHT; ++ht) {
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) asm volatile("" : "+v"(qw[ht][kc]));  // loaded: the wait above was vmcnt(0)
+      }
+#pragma unroll
+      for (int ht = 0; ht < kHT; ++ht) {
+        const bool live = ht * 16U + dec.c < a.group;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc)
+          dec.qb[ht][kc] = __builtin_bit_cast(vec8, live ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
+      }
     }
     for (uint32_t n = 0; n < my_n; n += S) {
 #pragma unroll
@@ -1547,7 +1573,8 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
             dec.zero_dead_rows(vtile, t0);
           }
           wave_fence_lds();
-          const f32x4 sc = dec.qk(tl[i]);
+          f32x4 sc[kHT];
+          dec.qk(tl[i], sc);
           dec.softmax_pv(sc, t0, vtile);
           wait_lds_reads();
           dec.issue(tl[i], nx[i], tn);
@@ -1559,26 +1586,34 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   }
 
-  float l = dec.lsum;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  const uint32_t h = dec.c;
-  const bool head_live = h < a.group;
+  float lt[kHT];
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht) {
+    float l = dec.lsum[ht];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    lt[ht] = l;
+  }
   if (kSplit == 1) {
-    if (head_live) store_wave_result<QE>(a, dec, seq, kvh, part, v_scale, l);
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      if (ht * 16U + dec.c < a.group) store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
+    }
     return;
   }
 
-  // Several waves split the partition: reduce through LDS.
+  // Several waves split the partition (one head tile): reduce through LDS.
+  const uint32_t h = dec.c;
+  const float l = lt[0];
   float (*red_o)[16][kDim] = reinterpret_cast<float (*)[16][kDim]>(tiles);
   __shared__ float red_ml[kSplit][16][2];
   __syncthreads();  // every wave is done with its V tiles
   if (dec.g == 0) {
-    red_ml[wave][h][0] = dec.m;
+    red_ml[wave][h][0] = dec.m[0];
     red_ml[wave][h][1] = l;
   }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&red_o[wave][h][dt * 16 + 4 * dec.g]) = dec.acc[dt];
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&red_o[wave][h][dt * 16 + 4 * dec.g]) = dec.acc[0][dt];
   __syncthreads();
   const uint32_t heads = min(a.group, 16U);
   for (uint32_t idx = threadIdx.x; idx < heads * kDim; idx += kSplit * 64) {
@@ -1609,14 +1644,14 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   }
 }
 
-template <typename QE, bool kFp8, int kSplit>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8>;
+  using Dec = StreamDecoder<QE, kFp8, kHT>;
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * Dec::kWaveBytes];
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
-  stream_item<QE, kFp8, kSplit>(a, tiles, item);
+  stream_item<QE, kFp8, kSplit, kHT>(a, tiles, item);
 }
 
 // kGroup consecutive work items per workgroup, one wave each and independent
@@ -2189,20 +2224,20 @@ int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stre
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
-template <typename QE, bool kFp8, int kSplit>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1>
 int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit>), dim3(static_cast<uint32_t>(grid)),
+  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit, kHT>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kSplit * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
 // The streaming kernel needs steps that stay inside one block (power-of-two
-// block size >= 16, partitions starting on multiples of 16), at most 16 query
-// heads per KV head, and per-lane byte offsets (15 pages + one row) that fit
-// in 31 bits.
+// block size >= 16, partitions starting on multiples of 16), at most 32 query
+// heads per KV head (two 16-head tiles per wave), and per-lane byte offsets
+// (15 pages + one row) that fit in 31 bits.
 bool stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
-  if (group > 16 || p.block_size < kStep) return false;
+  if (group > 32 || p.block_size < kStep) return false;
   if (parts > 1 && p.partition_tokens % kStep != 0) return false;
   const uint64_t es = cache_elem_size(p);
   const uint64_t limit = 1ULL << 31;
@@ -2322,7 +2357,9 @@ int run_typed(const Problem& p, hipStream_t stream) {
       // steps per wave, else run one wave per workgroup: there the number of
       // CUs in use matters more than co-locating heads. (16-wave groups
       // measured slower: they add no CUs, only contention within one.)
-      if (grid >= 4096) {
+      if (group > 16) {
+        status = fp8 ? launch_stream<QE, true, 1, 2>(args, grid, stream) : launch_stream<QE, false, 1, 2>(args, grid, stream);
+      } else if (grid >= 4096) {
         status = fp8 ? launch_stream_group<QE, true>(args, grid, stream) : launch_stream_group<QE, false>(args, grid, stream);
       } else if (steps < 8) {
         status = fp8 ? launch_stream<QE, true, 1>(args, grid, stream) : launch_stream<QE, false, 1>(args, grid, stream);
@@ -2660,7 +2697,7 @@ int loom_hip_paged_decode_attention_supports(
     *kernel_family = status != LOOM_HIP_SUCCESS ? ""
                      : !mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
                          ? "vector"
-                         : (query_heads / kv_heads <= 16 && block_size >= kStep) ? "mfma-stream"
+                         : (query_heads / kv_heads <= 32 && block_size >= kStep) ? "mfma-stream"
                                                                                   : "mfma";
   }
   return status;

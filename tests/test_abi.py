@@ -180,13 +180,15 @@ def test_capability_query():
     s, reason, fam = ops.supports(2, 0, 64, 32, 8, 128, 128, 21800, 8, 1024, 8192, 0.088)
     assert (s, fam) == (0, "mfma")
     s, reason, fam = ops.supports(1, 0, 64, 64, 2, 128, 128, 21800, 16, 512, 8192, 0.088)
+    assert (s, fam) == (0, "mfma-stream")  # 32 heads per KV head: two 16-head tiles per wave
+    s, reason, fam = ops.supports(1, 0, 64, 64, 2, 128, 128, 21800, 8, 1024, 8192, 0.088)
     assert (s, fam) == (0, "mfma")
     s, reason, fam = ops.supports(0, 0, 4, 8, 8, 64, 64, 64, 16, 16, 256, 0.125)
     assert (s, fam) == (0, "vector")
     s, reason, fam = ops.supports(2, 1, 128, 64, 8, 128, 128, 32768, 16, 256, 4096, 0.088)
     assert (s, fam) == (0, "mfma-stream")
     s, reason, fam = ops.supports(2, 0, 8, 32, 1, 128, 128, 65536, 16, 8192, 131072, 0.088)
-    assert (s, fam) == (0, "mfma")
+    assert (s, fam) == (0, "mfma-stream")
     s, reason, _ = ops.supports(7, 0, 4, 8, 8, 64, 64, 64, 16, 16, 256, 0.125)
     assert s == _native.UNSUPPORTED and "F32, FP16 and BF16" in reason
     s, reason, _ = ops.supports(2, 0, 4, 6, 4, 64, 64, 64, 16, 16, 256, 0.125)

@@ -267,6 +267,28 @@ def test_matrix_core_kernels_match_oracle(dtype, encoding, block_size, partition
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("encoding", ["native", "fp8"])
+@pytest.mark.parametrize("shape", [
+    (3, 32, 1, 128, 128, 16, [1100, 1, 530]),   # MQA group of 32: two full 16-head tiles
+    (3, 48, 2, 128, 128, 16, [17, 700, 1030]),  # group of 24: the second tile has 8 live heads
+])
+@pytest.mark.parametrize("partition_tokens", [512, 0])
+def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
+    """Groups of 17-32 query heads per KV head on the streaming kernel: both
+    16-head tiles in one wave, sharing the K and V reads."""
+    B, Hq, Hkv, D, Dv, bs, lengths = shape
+    case = case_from(shape, dtype, seed=61, cache_encoding=encoding, partition_tokens=partition_tokens)
+    _, _, fam = ops.supports(2, 0, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
+                             case.max_sequence_length, case.scale)
+    assert fam == "mfma-stream"
+    out, lse = workloads.run_case(case, return_lse=True)
+    torch.cuda.synchronize()
+    expected, want_lse = oracle_expected(case)
+    assert_parity(out, expected, dtype, f"tiles {shape} part{partition_tokens} {encoding}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
 def test_config1_f32_plumbing_full():
     case = workloads.config(1, DEV)
     out, lse = workloads.run_case(case, return_lse=True)
