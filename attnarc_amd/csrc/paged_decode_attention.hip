@@ -1721,14 +1721,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
         v1[j] = j < n && d + 1 < Dv ? src[1] : 0.0f;
       }
     }
-    float M = mp;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const float M = wave_max_dpp(mp);
     // A partition without tokens would hold m = -inf and contributes nothing.
     const float f = isfinite(mp) ? exp2f(mp - M) : 0.0f;
-    float L = lp * f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
+    const float L = wave_sum_dpp(lp * f);
     // Weight of partition p's stored output: f_p for sums, f_p l_p for normalised outputs.
     const float wgt = PartialOut<QE>::kNormalised ? f * lp : f;
     float o0 = 0.0f, o1 = 0.0f;
