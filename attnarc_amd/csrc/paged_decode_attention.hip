@@ -1098,13 +1098,21 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
 constexpr uint32_t kStep = 16;
 constexpr uint32_t kStepTileBytes = kStep * kTileRowBytes;  // 4 KiB
 
+// Chunk permutation of row t in a 16-bit V tile: 2 (t & 7) for 256-byte rows
+// (head size 128), 2 (t & 3) for 128-byte rows (head size 64), so that a
+// row's chunks stay inside the row.
+template <uint32_t kPitch>
+__host__ __device__ constexpr uint32_t vtile_swizzle(uint32_t t) {
+  return kPitch >= 256 ? (t & 7U) << 1 : (t & 3U) << 1;
+}
+
 // Byte offset of 16-byte chunk ch of row t in a 16-bit V tile (256-byte
 // rows): chunk ch sits at ch ^ 2 (t & 7). The transposed reads fetch 8 bytes
 // per lane from rows 4g .. 4g + 3 for two lane groups g at a time; XORing
 // with three row bits spreads those eight rows over all 64 banks.
 template <uint32_t kPitch = kTileRowBytes>
 __device__ __forceinline__ uint32_t vtile_off(uint32_t t, uint32_t ch) {
-  return t * kPitch + ((ch ^ ((t & 7U) << 1)) << 4);
+  return t * kPitch + ((ch ^ vtile_swizzle<kPitch>(t)) << 4);
 }
 
 template <int N>
@@ -1134,9 +1142,16 @@ constexpr int kStreamStagesFp8 = 2;
 
 // kHT: 16-query-head tiles per wave (1, or 2 for groups of 17-32 heads). The
 // tiles share each step's K operand fetches and V transposed reads.
-template <typename QE, bool kFp8, int kHT = 1>
+// kD: head size (= value head size): 128, or 64 for 16-bit caches, whose
+// 128-byte rows then take the FP8 path's DMA geometry (eight rows per
+// instruction) without a conversion.
+template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static constexpr uint32_t kPitch = kTileRowBytes;  // bytes between consecutive tokens' rows in a stage
+  static_assert(kD == kDim || (kD == 64 && !kFp8), "head size 128, or 64 with a 16-bit cache");
+  static constexpr bool kNarrow = kD == 64;                  // 16-bit rows of 128 bytes
+  static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
+  static constexpr int kDt = kD / 16;         // 16-dim PV tiles
+  static constexpr int kKc = kD / 32;         // 32-dim QK operand chunks
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
@@ -1145,11 +1160,11 @@ struct StreamDecoder {
   // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
   static constexpr int kStages = kFp8 ? kStreamStagesFp8 : kStreamStages;
   static constexpr uint32_t kF8TileBytes = kStep * kDim;  // 2 KiB
-  static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kStepTileBytes;
-  static constexpr uint32_t kVOff = kStepTileBytes;  // 16-bit: V within a stage
+  static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kStep * kPitch;
+  static constexpr uint32_t kVOff = kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
   static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStepTileBytes : 0);
-  static constexpr int kDmaPerStep = kFp8 ? 4 : 8;
+  static constexpr int kDmaPerStep = kFp8 || kNarrow ? 4 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -1165,8 +1180,8 @@ struct StreamDecoder {
   uint32_t f8_k_voff[2], f8_v_voff[2];  // FP8: lane's K / V DMA offsets, rows 8i .. 8i + 7
   float sl2;
 
-  vec8 qb[kHT][4];
-  f32x4 acc[kHT][8];  // O^T of tile ht: dims dt*16 + 4g + r, head 16 ht + c
+  vec8 qb[kHT][kKc];
+  f32x4 acc[kHT][kDt];  // O^T of tile ht: dims dt*16 + 4g + r, head 16 ht + c
   float m[kHT];       // running max (log2 units) of head 16 ht + c
   float lsum[kHT];    // partial denominator over this lane's tokens
 
@@ -1194,7 +1209,17 @@ struct StreamDecoder {
   // instruction, chunk L of row r at L ^ ((r >> 1) & 7), which keeps the K
   // operand reads and the V conversion reads bank-conflict free.
   __device__ __forceinline__ void init_offsets() {
-    if (kFp8) {
+    if (kNarrow) {
+      // 16-bit rows of 128 bytes: K chunk L of row r at L ^ ((r >> 1) & 7)
+      // (as FP8 K), V chunk L at L ^ vtile_swizzle(r).
+      const uint32_t row = lane >> 3;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t r = 8 * i + row;
+        f8_k_voff[i] = static_cast<uint32_t>(row * kstride_p) + (((lane & 7U) ^ ((r >> 1) & 7U)) << 4);
+        f8_v_voff[i] = static_cast<uint32_t>(row * vstride_p) + (((lane & 7U) ^ vtile_swizzle<kPitch>(r)) << 4);
+      }
+    } else if (kFp8) {
       const uint32_t row = lane >> 3;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -1217,7 +1242,13 @@ struct StreamDecoder {
   __device__ __forceinline__ void issue(uint8_t* stage, uint32_t blk, uint32_t t0) const {
     const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
-    if (kFp8) {
+    if (kNarrow) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        vm_load16_lds_sv(f8_v_voff[i], vb + 8 * i * vstride_p, stage + kVOff + i * 1024);
+    } else if (kFp8) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
 #pragma unroll
@@ -1236,7 +1267,10 @@ struct StreamDecoder {
   // dims); the half depends on g so that the two lane groups served together
   // read different banks.
   __device__ __forceinline__ vec8 k_operand(const uint8_t* stage, int kc) const {
-    if (kFp8) {
+    if (kNarrow) {
+      const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ ((c >> 1) & 7U);
+      return *reinterpret_cast<const vec8*>(stage + c * kPitch + chunk * 16);
+    } else if (kFp8) {
       const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ ((c >> 1) & 7U);
       const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kDim + chunk * 16 + ((kc ^ g) & 1U) * 8);
       return Ops::from_fp8(w.x, w.y);
@@ -1247,14 +1281,14 @@ struct StreamDecoder {
   }
 
   __device__ __forceinline__ void qk(const uint8_t* stage, f32x4 (&z)[kHT]) const {
-    vec8 kop[4];
+    vec8 kop[kKc];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) kop[kc] = k_operand(stage, kc);
+    for (int kc = 0; kc < kKc; ++kc) kop[kc] = k_operand(stage, kc);
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
       z[ht] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) z[ht] = Ops::mma(kop[kc], qb[ht][kc], z[ht]);
+      for (int kc = 0; kc < kKc; ++kc) z[ht] = Ops::mma(kop[kc], qb[ht][kc], z[ht]);
     }
   }
 
@@ -1284,11 +1318,11 @@ struct StreamDecoder {
   // step) may hold unwritten cache slots: zero them so P = 0 meets a finite V.
   __device__ __forceinline__ void zero_dead_rows(uint8_t* tile, uint32_t t0) const {
     if (t0 + kStep <= len) return;  // uniform
-    const uint32_t t = lane >> 2;   // 4 lanes per row, 64 bytes each
+    const uint32_t t = lane >> 2;   // 4 lanes per row, kPitch / 4 bytes each
     if (t0 + t >= len) {
-      u32x4* row = reinterpret_cast<u32x4*>(tile + t * kPitch + (lane & 3U) * 64);
+      u32x4* row = reinterpret_cast<u32x4*>(tile + t * kPitch + (lane & 3U) * (kPitch / 4));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
+      for (uint32_t i = 0; i < kPitch / 64; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
     }
   }
 
@@ -1312,7 +1346,7 @@ struct StreamDecoder {
         const float alpha = __builtin_amdgcn_exp2f(m[ht] - mn);
         lsum[ht] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[ht][dt] *= alpha;
+        for (int dt = 0; dt < kDt; ++dt) acc[ht][dt] *= alpha;
         m[ht] = mn;
       }
       float p[4];
@@ -1327,7 +1361,7 @@ struct StreamDecoder {
     const uint32_t k = c >> 2, q = c & 3U;
     lds_u8* base = (lds_u8*)tile;
 #pragma unroll
-    for (uint32_t dt = 0; dt < 8; ++dt) {
+    for (uint32_t dt = 0; dt < kDt; ++dt) {
       const uint32_t off = vtile_off<kPitch>(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
       const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
 #pragma unroll
@@ -1428,12 +1462,13 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
 template <typename QE, typename Dec>
 __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec& dec, int ht, uint32_t seq,
                                                   uint32_t head0, uint32_t part, float v_scale, float l) {
+  constexpr uint32_t D = Dec::kDt * 16;
   const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + head0 + dec.c;
   if (a.parts == 1) {
     const float inv = v_scale / l;
-    uint16_t* o = static_cast<uint16_t*>(a.output) + row * kDim + 4 * dec.g;
+    uint16_t* o = static_cast<uint16_t*>(a.output) + row * D + 4 * dec.g;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < Dec::kDt; ++dt) {
       uint32_t w0 = QE::from_f(dec.acc[ht][dt][0] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[ht][dt][1] * inv)) << 16);
       uint32_t w1 = QE::from_f(dec.acc[ht][dt][2] * inv) | (static_cast<uint32_t>(QE::from_f(dec.acc[ht][dt][3] * inv)) << 16);
       *reinterpret_cast<uint2*>(o + dt * 16) = make_uint2(w0, w1);
@@ -1443,7 +1478,7 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
     const uint64_t state = row * a.parts + part;
     const float inv_l = 1.0f / l;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) put_partial4<QE>(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
+    for (int dt = 0; dt < Dec::kDt; ++dt) put_partial4<QE>(a, state * D + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
     if (dec.g == 0) {
       a.ws_ml[state * 2] = dec.m[ht];
       a.ws_ml[state * 2 + 1] = l;
@@ -1456,10 +1491,10 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
 // partial-state stores. `tiles` holds kSplit waves' LDS (Dec::kWaveBytes
 // each); after the step loop the same memory holds each wave's O (16 heads x
 // 128 dims F32 = 8 KiB) for the cross-wave reduction.
-template <typename QE, bool kFp8, int kSplit, int kHT = 1>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim>
 __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
   static_assert(kHT == 1 || kSplit == 1, "two head tiles run one wave per item");
-  using Dec = StreamDecoder<QE, kFp8, kHT>;
+  using Dec = StreamDecoder<QE, kFp8, kHT, kD>;
   using vec8 = typename Dec::vec8;
   constexpr int S = Dec::kStages;
   const uint32_t kvh = item.kvh;
@@ -1467,7 +1502,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   const uint32_t seq = item.seq;
   const uint32_t len = item.len;
   const uint32_t p0 = part * a.partition_tokens;
-  static_assert(kSplit * Dec::kWaveBytes >= kSplit * 16 * kDim * sizeof(float),
+  static_assert(kSplit * Dec::kWaveBytes >= kSplit * 16 * kD * sizeof(float),
                 "the cross-wave reduction reuses the stages");
 
   Dec dec(a);
@@ -1510,7 +1545,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     dec.m[ht] = -INFINITY;
     dec.lsum[ht] = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) dec.acc[ht][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int dt = 0; dt < Dec::kDt; ++dt) dec.acc[ht][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   if (my_n > 0) {
@@ -1537,9 +1572,13 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       for (int ht = 0; ht < kHT; ++ht) {
         const uint32_t h = min(ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
         const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
-                               (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kDim;
+                               (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kD;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
+          if (kc >= Dec::kKc) {
+            qw[ht][kc] = u32x4{0U, 0U, 0U, 0U};
+            continue;
+          }
           const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
           vm_load16(qw[ht][kc], qrow + dim);
         }
@@ -1554,7 +1593,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       for (int ht = 0; ht < kHT; ++ht) {
         const bool live = ht * 16U + dec.c < a.group;
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc)
+        for (int kc = 0; kc < Dec::kKc; ++kc)
           dec.qb[ht][kc] = __builtin_bit_cast(vec8, live ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
       }
     }
@@ -1605,7 +1644,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   // Several waves split the partition (one head tile): reduce through LDS.
   const uint32_t h = dec.c;
   const float l = lt[0];
-  float (*red_o)[16][kDim] = reinterpret_cast<float (*)[16][kDim]>(tiles);
+  float (*red_o)[16][kD] = reinterpret_cast<float (*)[16][kD]>(tiles);
   __shared__ float red_ml[kSplit][16][2];
   __syncthreads();  // every wave is done with its V tiles
   if (dec.g == 0) {
@@ -1613,11 +1652,11 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     red_ml[wave][h][1] = l;
   }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(&red_o[wave][h][dt * 16 + 4 * dec.g]) = dec.acc[0][dt];
+  for (int dt = 0; dt < Dec::kDt; ++dt) *reinterpret_cast<f32x4*>(&red_o[wave][h][dt * 16 + 4 * dec.g]) = dec.acc[0][dt];
   __syncthreads();
   const uint32_t heads = min(a.group, 16U);
-  for (uint32_t idx = threadIdx.x; idx < heads * kDim; idx += kSplit * 64) {
-    const uint32_t hl = idx / kDim, d = idx % kDim;
+  for (uint32_t idx = threadIdx.x; idx < heads * kD; idx += kSplit * 64) {
+    const uint32_t hl = idx / kD, d = idx % kD;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kSplit; ++w) M = fmaxf(M, red_ml[w][hl][0]);
@@ -1631,11 +1670,11 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     O *= v_scale;
     const uint64_t row = static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + hl;
     if (a.parts == 1) {
-      static_cast<uint16_t*>(a.output)[row * kDim + d] = QE::from_f(O / L);
+      static_cast<uint16_t*>(a.output)[row * kD + d] = QE::from_f(O / L);
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
       const uint64_t state = row * a.parts + part;
-      put_partial<QE>(a, state * kDim + d, O, 1.0f / L);
+      put_partial<QE>(a, state * kD + d, O, 1.0f / L);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
         a.ws_ml[state * 2 + 1] = L;
@@ -1644,14 +1683,14 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   }
 }
 
-template <typename QE, bool kFp8, int kSplit, int kHT = 1>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8, kHT>;
+  using Dec = StreamDecoder<QE, kFp8, kHT, kD>;
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * Dec::kWaveBytes];
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
-  stream_item<QE, kFp8, kSplit, kHT>(a, tiles, item);
+  stream_item<QE, kFp8, kSplit, kHT, kD>(a, tiles, item);
 }
 
 // kGroup consecutive work items per workgroup, one wave each and independent
@@ -1662,15 +1701,15 @@ void decode_stream_kernel(DecodeArgs a) {
 // serves faster than the same rows requested from CUs on different XCDs.
 constexpr int kStreamGroup = 4;
 
-template <typename QE, bool kFp8, int kGroup>
+template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim>
 __global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_group_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8>;
+  using Dec = StreamDecoder<QE, kFp8, 1, kD>;
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * Dec::kWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
   if (!item.valid) return;  // per wave: nothing below waits on the other waves
-  stream_item<QE, kFp8, 1>(a, tiles + wave * Dec::kWaveBytes, item);
+  stream_item<QE, kFp8, 1, 1, kD>(a, tiles + wave * Dec::kWaveBytes, item);
 }
 
 // ---------------------------------------------------------------------------
@@ -2211,19 +2250,19 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
-template <typename QE, bool kFp8>
+template <typename QE, bool kFp8, uint32_t kD = kDim>
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   const uint64_t groups = (items + kStreamGroup - 1) / kStreamGroup;
-  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kStreamGroup>), dim3(static_cast<uint32_t>(groups)),
+  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kStreamGroup, kD>), dim3(static_cast<uint32_t>(groups)),
                      dim3(kStreamGroup * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
-template <typename QE, bool kFp8, int kSplit, int kHT = 1>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim>
 int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit, kHT>), dim3(static_cast<uint32_t>(grid)),
+  hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit, kHT, kD>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kSplit * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
@@ -2238,6 +2277,26 @@ bool stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   const uint64_t es = cache_elem_size(p);
   const uint64_t limit = 1ULL << 31;
   return 15 * p.k_page * es + 256 < limit && 15 * p.v_page * es + 256 < limit;
+}
+
+// Head size 64 with a 16-bit cache on the streaming kernel: 16-bit queries,
+// native cache, D = Dv = 64, power-of-two blocks, 16-byte aligned bases and
+// strides, and the streaming kernel's own step and offset conditions.
+bool narrow_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
+                  uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE && head_size == 64 &&
+         value_head_size == 64 && query_heads / kv_heads <= 32 && is_pow2(block_size) && block_size >= kStep;
+}
+
+bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
+  if (!narrow_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
+                    p.block_size))
+    return false;
+  const uint64_t strides[] = {p.k_block, p.k_page, p.k_head, p.v_block, p.v_page, p.v_head};
+  for (uint64_t st : strides) {
+    if ((st * 2) % 16 != 0) return false;
+  }
+  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) && stream_eligible(p, parts, group);
 }
 
 
@@ -2336,9 +2395,31 @@ int run_typed(const Problem& p, hipStream_t stream) {
   args.score_scale_log2 = p.scale * kLog2e;
 
   int status = LOOM_HIP_SUCCESS;
-  bool use_mfma = false;
-  if constexpr (!std::is_same<QE, F32Elem>::value) use_mfma = mfma_eligible(p);
-  if (use_mfma) {
+  bool use_narrow = false, use_mfma = false;
+  if constexpr (!std::is_same<QE, F32Elem>::value) {
+    use_narrow = narrow_stream_eligible(p, parts, group);
+    use_mfma = !use_narrow && mfma_eligible(p);
+  }
+  if (use_narrow) {
+    if constexpr (!std::is_same<QE, F32Elem>::value) {
+      // Head size 64, 16-bit cache: the streaming kernel with 128-byte rows,
+      // in the launch shapes of the head-size-128 path below.
+      const uint64_t grid = parts * p.kv_heads * static_cast<uint64_t>(p.sequences);
+      if (grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
+        return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
+      args.grid_y = p.kv_heads;
+      const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
+      if (group > 16) {
+        status = launch_stream<QE, false, 1, 2, 64>(args, grid, stream);
+      } else if (grid >= 4096) {
+        status = launch_stream_group<QE, false, 64>(args, grid, stream);
+      } else if (steps < 8) {
+        status = launch_stream<QE, false, 1, 1, 64>(args, grid, stream);
+      } else {
+        status = launch_stream<QE, false, 4, 1, 64>(args, grid, stream);
+      }
+    }
+  } else if (use_mfma) {
     if constexpr (!std::is_same<QE, F32Elem>::value) {
     const uint64_t grid = parts * p.kv_heads * static_cast<uint64_t>(p.sequences);
     if (grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
@@ -2691,6 +2772,9 @@ int loom_hip_paged_decode_attention_supports(
   if (reason != nullptr) *reason = why;
   if (kernel_family != nullptr) {
     *kernel_family = status != LOOM_HIP_SUCCESS ? ""
+                     : narrow_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
+                                    block_size)
+                         ? "mfma-stream"
                      : !mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
                          ? "vector"
                          : (query_heads / kv_heads <= 32 && block_size >= kStep) ? "mfma-stream"

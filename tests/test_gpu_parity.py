@@ -289,6 +289,29 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+@pytest.mark.parametrize("shape,partition_tokens", [
+    ((4, 32, 8, 64, 64, 16, [700, 1, 33, 2050]), 512),   # split over 4 waves, partial last steps
+    ((4, 32, 8, 64, 64, 32, [700, 1, 33, 2050]), 64),    # 64-token partitions, 32-token blocks
+    ((3, 16, 2, 64, 64, 16, [90, 17, 300]), 0),          # single partition, 8 heads per KV head
+    ((3, 32, 1, 64, 64, 16, [1100, 1, 530]), 512),       # MQA group of 32: two head tiles per wave
+    ((256, 16, 8, 64, 64, 16, [300 - (i % 37) for i in range(256)]), 128),  # >= 4096 items: grouped launch
+])
+def test_stream_kernel_head_size_64(dtype, layout, shape, partition_tokens):
+    """Head size 64 with a 16-bit cache on the streaming kernel (128-byte rows)."""
+    B, Hq, Hkv, D, Dv, bs, lengths = shape
+    case = case_from(shape, dtype, seed=71, layout=layout, partition_tokens=partition_tokens)
+    _, _, fam = ops.supports(2, 0, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
+                             case.max_sequence_length, case.scale)
+    assert fam == "mfma-stream"
+    out, lse = workloads.run_case(case, return_lse=True)
+    torch.cuda.synchronize()
+    expected, want_lse = oracle_expected(case)
+    assert_parity(out, expected, dtype, f"d64 {shape[:6]} part{partition_tokens} {layout}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
 def test_config1_f32_plumbing_full():
     case = workloads.config(1, DEV)
     out, lse = workloads.run_case(case, return_lse=True)
