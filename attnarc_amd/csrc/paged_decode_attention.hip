@@ -7,25 +7,29 @@
 // crates/loom-cuda-sys/cuda/include/loom_cuda.h:175-250 plus extensions.
 //
 // Kernels
-//   decode_mfma_kernel   D = Dv = 128, 16-bit query, native 16-bit or FP8
-//                        E4M3FN cache, power-of-two block size. One
-//                        workgroup per (partition, KV head, sequence); each
-//                        wave streams 32-token chunks: K is loaded straight
-//                        into the MFMA operand layout, V is staged through a
-//                        swizzled LDS tile and read back transposed, and both
-//                        QK^T and PV run on v_mfma_f32_16x16x32_{bf16,f16}
-//                        with the whole GQA group (up to 32 heads) held in
-//                        registers, so every K/V byte is read once.
-//   decode_vector_kernel any shape and dtype (including F32); fp32 VALU with
-//                        wave-wide reductions. Covers the general contract.
-//   merge_kernel         stable log-sum-exp merge of per-partition states
+//   decode_stream_kernel / decode_stream_group_kernel
+//                        the main path: 16-bit query, D = Dv = 128 (native or
+//                        FP8 E4M3FN cache) or 64 (native 16-bit cache), up
+//                        to 32 query heads per KV head, power-of-two blocks
+//                        >= 16. One wave per (sequence, partition, KV head)
+//                        item streams 16-token steps: K and V rows go to LDS
+//                        by DMA (XOR-swizzled), QK^T and PV run on MFMA with
+//                        the group's heads as the N dimension. Full grids
+//                        put four adjacent-head items in one workgroup.
+//   decode_mfma_kernel   the same head layout with 32-token chunks and K in
+//                        registers, for block sizes below 16 and partitions
+//                        that are not a multiple of 16 tokens.
+//   decode_vector_kernel any shape and dtype (including F32); fp32 VALU on
+//                        64-token tiles. Covers the general contract.
+//   merge_kernel / merge_rows128_kernel / merge_wide_kernel
+//                        stable log-sum-exp merge of per-partition states
 //                        (the math of paged_decode_attention.cu:780-852).
 //
-// Both decode kernels keep an online softmax in base-2 units (scores are
-// multiplied by scale * log2(e)) and reduce the waves of a workgroup in LDS.
-// A workgroup whose partition is the whole sequence writes the output (and
-// optional LSE) directly; otherwise it writes (m, l, o[Dv]) to the caller's
-// F32 workspace and merge_kernel finishes.
+// The decode kernels keep an online softmax in base-2 units (scores are
+// multiplied by scale * log2(e)). A work item whose partition is the whole
+// sequence writes the output (and optional LSE) directly; otherwise it
+// writes (m, l) and its partial output to the caller's F32 workspace and a
+// merge kernel finishes.
 
 #include <hip/hip_runtime.h>
 
