@@ -1146,13 +1146,16 @@ constexpr int kStreamStagesFp8 = 2;
 
 // kHT: 16-query-head tiles per wave (1, or 2 for groups of 17-32 heads). The
 // tiles share each step's K operand fetches and V transposed reads.
-// kD: head size (= value head size): 128, or 64 for 16-bit caches, whose
+// kD: head size (= value head size): 128; 64 for 16-bit caches, whose
 // 128-byte rows then take the FP8 path's DMA geometry (eight rows per
-// instruction) without a conversion.
+// instruction) without a conversion; 256 for 16-bit caches and one head tile
+// (512-byte rows, two per DMA instruction).
 template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static_assert(kD == kDim || (kD == 64 && !kFp8), "head size 128, or 64 with a 16-bit cache");
+  static_assert(kD == kDim || (kD == 64 && !kFp8) || (kD == 256 && !kFp8 && kHT == 1),
+                "head size 128; 64 or 256 (one head tile) with a 16-bit cache");
   static constexpr bool kNarrow = kD == 64;                  // 16-bit rows of 128 bytes
+  static constexpr bool kWide = kD == 256;                   // 16-bit rows of 512 bytes
   static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
   static constexpr int kDt = kD / 16;         // 16-dim PV tiles
   static constexpr int kKc = kD / 32;         // 32-dim QK operand chunks
@@ -1168,7 +1171,7 @@ struct StreamDecoder {
   static constexpr uint32_t kVOff = kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
   static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStepTileBytes : 0);
-  static constexpr int kDmaPerStep = kFp8 || kNarrow ? 4 : 8;
+  static constexpr int kDmaPerStep = kFp8 || kNarrow ? 4 : kWide ? 16 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -1182,6 +1185,7 @@ struct StreamDecoder {
   uint32_t k_voff[4];  // 16-bit: lane's K DMA offset for rows 4i..4i+3
   uint32_t v_voff[2];  // 16-bit: lane's V DMA offset for even / odd 4-row groups
   uint32_t f8_k_voff[2], f8_v_voff[2];  // FP8: lane's K / V DMA offsets, rows 8i .. 8i + 7
+  uint32_t w_voff[kWide ? 16 : 1];      // head size 256: K offsets (rows 2i, 2i + 1), then V
   float sl2;
 
   vec8 qb[kHT][kKc];
@@ -1213,7 +1217,17 @@ struct StreamDecoder {
   // instruction, chunk L of row r at L ^ ((r >> 1) & 7), which keeps the K
   // operand reads and the V conversion reads bank-conflict free.
   __device__ __forceinline__ void init_offsets() {
-    if (kNarrow) {
+    if constexpr (kWide) {
+      // 512-byte rows, two per instruction: K chunk L of row r at L ^ (r & 15),
+      // V chunk L at L ^ vtile_swizzle(r) (the bank pattern of 256-byte rows).
+      const uint32_t row = lane >> 5;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t r = 2 * i + row;
+        w_voff[i] = static_cast<uint32_t>(row * kstride_p) + (((lane & 31U) ^ (r & 15U)) << 4);
+        w_voff[8 + i] = static_cast<uint32_t>(row * vstride_p) + (((lane & 31U) ^ vtile_swizzle<kPitch>(r)) << 4);
+      }
+    } else if (kNarrow) {
       // 16-bit rows of 128 bytes: K chunk L of row r at L ^ ((r >> 1) & 7)
       // (as FP8 K), V chunk L at L ^ vtile_swizzle(r).
       const uint32_t row = lane >> 3;
@@ -1246,7 +1260,12 @@ struct StreamDecoder {
   __device__ __forceinline__ void issue(uint8_t* stage, uint32_t blk, uint32_t t0) const {
     const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
-    if (kNarrow) {
+    if constexpr (kWide) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vm_load16_lds_sv(w_voff[i], kb + 2 * i * kstride_p, stage + i * 1024);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vm_load16_lds_sv(w_voff[8 + i], vb + 2 * i * vstride_p, stage + kVOff + i * 1024);
+    } else if (kNarrow) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
 #pragma unroll
@@ -1571,27 +1590,23 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     // Q is loaded after the first steps' K/V and waited for together with
     // them, so a wave's start costs one memory round trip, not two.
     {
-      u32x4 qw[kHT][4];
+      u32x4 qw[kHT][Dec::kKc];
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) {
         const uint32_t h = min(ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
         const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
                                (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kD;
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-          if (kc >= Dec::kKc) {
-            qw[ht][kc] = u32x4{0U, 0U, 0U, 0U};
-            continue;
-          }
+        for (int kc = 0; kc < Dec::kKc; ++kc) {
           const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
           vm_load16(qw[ht][kc], qrow + dim);
         }
       }
-      vm_wait_all(qw[0]);
+      asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 #pragma unroll
-      for (int ht = 1; ht < kHT; ++ht) {
+      for (int ht = 0; ht < kHT; ++ht) {
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) asm volatile("" : "+v"(qw[ht][kc]));  // loaded: the wait above was vmcnt(0)
+        for (int kc = 0; kc < Dec::kKc; ++kc) asm volatile("" : "+v"(qw[ht][kc]));  // loaded: the wait above was vmcnt(0)
       }
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) {
@@ -2254,12 +2269,12 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
-template <typename QE, bool kFp8, uint32_t kD = kDim>
+template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup>
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  const uint64_t groups = (items + kStreamGroup - 1) / kStreamGroup;
-  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kStreamGroup, kD>), dim3(static_cast<uint32_t>(groups)),
-                     dim3(kStreamGroup * 64), 0, stream, args);
+  const uint64_t groups = (items + kGroup - 1) / kGroup;
+  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD>), dim3(static_cast<uint32_t>(groups)),
+                     dim3(kGroup * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
@@ -2292,9 +2307,19 @@ bool narrow_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, u
          value_head_size == 64 && query_heads / kv_heads <= 32 && is_pow2(block_size) && block_size >= kStep;
 }
 
+// Head size 256 with a 16-bit cache: as head size 64, with at most 16 query
+// heads per KV head (one head tile per wave).
+bool wide_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
+                uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE && head_size == 256 &&
+         value_head_size == 256 && query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
+}
+
 bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   if (!narrow_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
-                    p.block_size))
+                    p.block_size) &&
+      !wide_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
+                  p.block_size))
     return false;
   const uint64_t strides[] = {p.k_block, p.k_page, p.k_head, p.v_block, p.v_page, p.v_head};
   for (uint64_t st : strides) {
@@ -2406,14 +2431,23 @@ int run_typed(const Problem& p, hipStream_t stream) {
   }
   if (use_narrow) {
     if constexpr (!std::is_same<QE, F32Elem>::value) {
-      // Head size 64, 16-bit cache: the streaming kernel with 128-byte rows,
-      // in the launch shapes of the head-size-128 path below.
+      // Head size 64 or 256, 16-bit cache: the streaming kernel with 128- or
+      // 512-byte rows, in the launch shapes of the head-size-128 path below.
       const uint64_t grid = parts * p.kv_heads * static_cast<uint64_t>(p.sequences);
       if (grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
         return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
       args.grid_y = p.kv_heads;
       const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
-      if (group > 16) {
+      if (p.head_size == 256) {
+        // 32 KiB of LDS per wave: two items per grouped workgroup.
+        if (grid >= 4096) {
+          status = launch_stream_group<QE, false, 256, 2>(args, grid, stream);
+        } else if (steps < 8) {
+          status = launch_stream<QE, false, 1, 1, 256>(args, grid, stream);
+        } else {
+          status = launch_stream<QE, false, 4, 1, 256>(args, grid, stream);
+        }
+      } else if (group > 16) {
         status = launch_stream<QE, false, 1, 2, 64>(args, grid, stream);
       } else if (grid >= 4096) {
         status = launch_stream_group<QE, false, 64>(args, grid, stream);
@@ -2777,7 +2811,9 @@ int loom_hip_paged_decode_attention_supports(
   if (kernel_family != nullptr) {
     *kernel_family = status != LOOM_HIP_SUCCESS ? ""
                      : narrow_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
-                                    block_size)
+                                    block_size) ||
+                               wide_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
+                                          block_size)
                          ? "mfma-stream"
                      : !mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
                          ? "vector"
