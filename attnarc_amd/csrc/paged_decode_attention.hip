@@ -72,8 +72,8 @@ struct DecodeArgs {
   const int32_t* sequence_lengths;
   void* output;
   float* lse;
-  float* ws_ml;  // [rows][parts][2] = (m in log2 units, l)
-  void* ws_o;    // [rows][parts][Dv] partial outputs (PartialOut<QE> encoding)
+  float* ws_ml;  // [sequences][parts][query_heads][2] = (m in log2 units, l)
+  void* ws_o;    // [sequences][parts][query_heads][Dv] partial outputs (PartialOut<QE> encoding)
   uint64_t k_block, k_page, k_head;  // element strides of the key cache
   uint64_t v_block, v_page, v_head;  // element strides of the value cache
   uint32_t query_heads;
@@ -91,6 +91,15 @@ struct DecodeArgs {
   uint32_t sequences;
   float score_scale_log2;  // scale * log2(e)
 };
+
+// Index of the split-K state of output row (sequence, query head) = row and
+// partition part. States are ordered [sequence][partition][query head], so
+// the states one workgroup of adjacent KV heads writes for a partition are
+// contiguous (whole cache lines for the (m, l) pairs).
+__device__ __forceinline__ uint64_t state_of(const DecodeArgs& a, uint64_t row, uint32_t part) {
+  const uint64_t seq = row / a.query_heads;
+  return (seq * a.parts + part) * a.query_heads + (row - seq * a.query_heads);
+}
 
 // ---------------------------------------------------------------------------
 // Element types.
@@ -513,7 +522,7 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
       static_cast<QT*>(a.output)[row * Dv + d] = QE::from_f(O / L);
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
-      const uint64_t state = row * a.parts + part;
+      const uint64_t state = state_of(a, row, part);
       put_partial<QE>(a, state * partial_stride<QE>(Dv) + d, O, 1.0f / L);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
@@ -1011,7 +1020,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
         }
         if (a.lse != nullptr && dec.g == 0) a.lse[row] = (M + log2f(L)) * kLn2;
       } else {
-        const uint64_t state = row * a.parts + part;
+        const uint64_t state = state_of(a, row, part);
         const float inv_l = 1.0f / L;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
@@ -1064,7 +1073,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
         static_cast<uint16_t*>(a.output)[row * kDim + d] = QE::from_f(O / L);
         if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
       } else {
-        const uint64_t state = row * a.parts + part;
+        const uint64_t state = state_of(a, row, part);
         put_partial<QE>(a, state * kDim + d, O, 1.0f / L);
         if (d == 0) {
           a.ws_ml[state * 2] = M;
@@ -1498,7 +1507,7 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
     }
     if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m[ht] + log2f(l)) * kLn2;
   } else {
-    const uint64_t state = row * a.parts + part;
+    const uint64_t state = state_of(a, row, part);
     const float inv_l = 1.0f / l;
 #pragma unroll
     for (int dt = 0; dt < Dec::kDt; ++dt) put_partial4<QE>(a, state * D + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
@@ -1692,7 +1701,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       static_cast<uint16_t*>(a.output)[row * kD + d] = QE::from_f(O / L);
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
-      const uint64_t state = row * a.parts + part;
+      const uint64_t state = state_of(a, row, part);
       put_partial<QE>(a, state * kD + d, O, 1.0f / L);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
@@ -1753,21 +1762,24 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
   const uint32_t seq = row / a.query_heads;
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
   const uint32_t n = min(min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts), kParts);
-  const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
+  // partition j of this row is state state_of(a, row, 0) + j * query_heads
+  const uint64_t s0 = state_of(a, row, 0);
+  const uint64_t sstride = a.query_heads;
+  const float* ml = a.ws_ml + s0 * 2;
   using PT = typename PartialOut<QE>::T;
   const uint32_t Dv = a.value_head_size;
   const uint32_t ps = partial_stride<QE>(Dv);
-  const PT* os = static_cast<const PT*>(a.ws_o) + static_cast<uint64_t>(row) * a.parts * ps;
+  const PT* os = static_cast<const PT*>(a.ws_o) + s0 * ps;
   QT* out = static_cast<QT*>(a.output) + static_cast<uint64_t>(row) * Dv;
 
-  const float mp = lane < n ? ml[2 * lane] : -INFINITY;
-  const float lp = lane < n ? ml[2 * lane + 1] : 0.0f;
+  const float mp = lane < n ? ml[2 * sstride * lane] : -INFINITY;
+  const float lp = lane < n ? ml[2 * sstride * lane + 1] : 0.0f;
   for (uint32_t d0 = 0; d0 < Dv; d0 += 128) {
     const uint32_t d = d0 + 2 * lane;
     float v0[kParts], v1[kParts];
 #pragma unroll
     for (uint32_t j = 0; j < kParts; ++j) {
-      const PT* src = os + static_cast<uint64_t>(j) * ps + d;
+      const PT* src = os + static_cast<uint64_t>(j) * sstride * ps + d;
       if constexpr (PartialOut<QE>::kNormalised) {
         // Both dims in one aligned 4-byte word (the row stride is even; the
         // padding element past an odd Dv is never used).
@@ -1821,16 +1833,20 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   const uint32_t seq = row / a.query_heads;
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
   const uint32_t n = (len + a.partition_tokens - 1) / a.partition_tokens;
-  const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
+  // partition p of this row is state state_of(a, row, 0) + p * query_heads
+  const uint64_t s0 = state_of(a, row, 0);
+  const uint64_t sstride = a.query_heads;
+  const float* ml = a.ws_ml + s0 * 2;
   using PT = typename PartialOut<QE>::T;
   const uint32_t ps = partial_stride<QE>(a.value_head_size);
-  const PT* os = static_cast<const PT*>(a.ws_o) + static_cast<uint64_t>(row) * a.parts * ps;
+  const uint64_t pstride = sstride * ps;  // elements between partitions' partial outputs
+  const PT* os = static_cast<const PT*>(a.ws_o) + s0 * ps;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63U;
   const uint32_t wave = tid >> 6;
 
   float M = -INFINITY;
-  for (uint32_t p = tid; p < n; p += kMergeThreads) M = fmaxf(M, ml[2 * p]);
+  for (uint32_t p = tid; p < n; p += kMergeThreads) M = fmaxf(M, ml[2 * sstride * p]);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
   if (lane == 0) red[wave] = M;
@@ -1841,7 +1857,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   __syncthreads();
 
   float Lp = 0.0f;
-  for (uint32_t p = tid; p < n; p += kMergeThreads) Lp = fmaf(ml[2 * p + 1], exp2f(ml[2 * p] - M), Lp);
+  for (uint32_t p = tid; p < n; p += kMergeThreads)
+    Lp = fmaf(ml[2 * sstride * p + 1], exp2f(ml[2 * sstride * p] - M), Lp);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) Lp += __shfl_xor(Lp, off, 64);
   if (lane == 0) red[wave] = Lp;
@@ -1872,16 +1889,16 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
       const uint32_t wn = min(kMergeWindow, n - w0);
       __syncthreads();
       for (uint32_t p = tid; p < wn; p += kMergeThreads) {
-        const float f = exp2f(ml[2 * (w0 + p)] - M);
-        factor[p] = PartialOut<QE>::kNormalised ? f * ml[2 * (w0 + p) + 1] : f;  // weight of the stored output
+        const float f = exp2f(ml[2 * sstride * (w0 + p)] - M);
+        factor[p] = PartialOut<QE>::kNormalised ? f * ml[2 * sstride * (w0 + p) + 1] : f;  // weight of the stored output
       }
       __syncthreads();
       uint32_t p = wave;
       for (; p + 3 * kMergeWaves < wn; p += 4 * kMergeWaves) {
-        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * ps;
-        const PT* o1 = o0 + kMergeWaves * static_cast<uint64_t>(ps);
-        const PT* o2 = o1 + kMergeWaves * static_cast<uint64_t>(ps);
-        const PT* o3 = o2 + kMergeWaves * static_cast<uint64_t>(ps);
+        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * pstride;
+        const PT* o1 = o0 + kMergeWaves * pstride;
+        const PT* o2 = o1 + kMergeWaves * pstride;
+        const PT* o3 = o2 + kMergeWaves * pstride;
         float a0, b0, a1, b1, a2, b2, a3, b3;
         pair(o0, a0, b0);
         pair(o1, a1, b1);
@@ -1899,7 +1916,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
         acc_b = fmaf(b3, f3, acc_b);
       }
       for (; p < wn; p += kMergeWaves) {
-        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * ps;
+        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * pstride;
         float a0, b0;
         pair(o0, a0, b0);
         acc_a = fmaf(a0, factor[p], acc_a);
@@ -1943,8 +1960,11 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
   const uint32_t seq = row / a.query_heads;
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
   const uint32_t n = min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts);  // <= 256
-  const float* ml = a.ws_ml + static_cast<uint64_t>(row) * a.parts * 2;
-  const uint16_t* os = static_cast<const uint16_t*>(a.ws_o) + static_cast<uint64_t>(row) * a.parts * kMergeFastDim;
+  // partition p of this row is state state_of(a, row, 0) + p * query_heads
+  const uint64_t s0 = state_of(a, row, 0);
+  const uint64_t sstride = a.query_heads;
+  const float* ml = a.ws_ml + s0 * 2;
+  const uint16_t* os = static_cast<const uint16_t*>(a.ws_o) + s0 * kMergeFastDim;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63U;
   const uint32_t wave = tid >> 6;
@@ -1955,11 +1975,11 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
 #pragma unroll
   for (uint32_t i = 0; i < kPerThread; ++i) {
     const uint32_t p = g + kGroups * i;
-    ov[i] = p < n ? *reinterpret_cast<const uint4*>(os + static_cast<uint64_t>(p) * kMergeFastDim + 8 * c)
+    ov[i] = p < n ? *reinterpret_cast<const uint4*>(os + static_cast<uint64_t>(p) * sstride * kMergeFastDim + 8 * c)
                   : make_uint4(0U, 0U, 0U, 0U);
   }
-  const float m = tid < n ? ml[2 * tid] : -INFINITY;
-  const float lp = tid < n ? ml[2 * tid + 1] : 0.0f;
+  const float m = tid < n ? ml[2 * sstride * tid] : -INFINITY;
+  const float lp = tid < n ? ml[2 * sstride * tid + 1] : 0.0f;
 
   float M = wave_max_dpp(m);
   if (lane == 0) red[wave] = M;
