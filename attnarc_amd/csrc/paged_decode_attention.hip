@@ -2459,17 +2459,20 @@ int run_typed(const Problem& p, hipStream_t stream) {
       args.grid_y = p.kv_heads;
       const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
       if (p.head_size == 256) {
-        // 32 KiB of LDS per wave: two items per grouped workgroup.
+        // 32 KiB of LDS per wave: two items per grouped workgroup, and the
+        // 4-wave split (129 KiB, one workgroup per CU) only for grids under
+        // 4 items per CU (measured: 1024-2048 items ran 11-15% faster as
+        // one wave per item; 128 items 1.6x slower).
         if (grid >= 4096) {
           status = launch_stream_group<QE, false, 256, 2>(args, grid, stream);
-        } else if (steps < 8) {
+        } else if (grid >= 1024 || steps < 8) {
           status = launch_stream<QE, false, 1, 1, 256>(args, grid, stream);
         } else {
           status = launch_stream<QE, false, 4, 1, 256>(args, grid, stream);
         }
       } else if (group > 16) {
         status = launch_stream<QE, false, 1, 2, 64>(args, grid, stream);
-      } else if (grid >= 4096) {
+      } else if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
         status = launch_stream_group<QE, false, 64>(args, grid, stream);
       } else if (steps < 8) {
         status = launch_stream<QE, false, 1, 1, 64>(args, grid, stream);
@@ -2486,15 +2489,17 @@ int run_typed(const Problem& p, hipStream_t stream) {
     const uint32_t chunks = (partition_tokens + kChunk - 1) / kChunk;
     const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
     if (stream_eligible(p, parts, group)) {
-      // A grid that fills the chip's 4096 wave slots (16 per CU) runs one
-      // wave per item, four items (adjacent KV heads) per workgroup. Smaller
-      // grids split each partition over 4 waves when that leaves at least 2
-      // steps per wave, else run one wave per workgroup: there the number of
-      // CUs in use matters more than co-locating heads. (16-wave groups
-      // measured slower: they add no CUs, only contention within one.)
+      // One wave per item, four items (adjacent KV heads) per workgroup, for
+      // grids of 4096 items or more, and from 1024 items (4 per CU) when
+      // partitions have at least 8 steps (measured 10% faster there than the
+      // 4-wave split). Smaller grids split each partition over 4 waves when
+      // that leaves at least 2 steps per wave, else run one wave per
+      // workgroup: there the number of CUs in use matters more than
+      // co-locating heads. (16-wave groups measured slower: they add no CUs,
+      // only contention within one.)
       if (group > 16) {
         status = fp8 ? launch_stream<QE, true, 1, 2>(args, grid, stream) : launch_stream<QE, false, 1, 2>(args, grid, stream);
-      } else if (grid >= 4096) {
+      } else if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
         status = fp8 ? launch_stream_group<QE, true>(args, grid, stream) : launch_stream_group<QE, false>(args, grid, stream);
       } else if (steps < 8) {
         status = fp8 ? launch_stream<QE, true, 1>(args, grid, stream) : launch_stream<QE, false, 1>(args, grid, stream);

@@ -265,6 +265,38 @@ def _config(index: int, device, seed, layout) -> DecodeCase:
     raise ValueError(f"unknown config {index}")
 
 
+_SHAPE_KEYS = {"B": int, "Hq": int, "Hkv": int, "D": int, "Dv": int, "L": int, "bs": int, "part": int,
+               "seed": int, "dtype": str, "kv": str, "layout": str}
+_DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def shape_case(spec: str, device) -> DecodeCase:
+    """A decode workload outside the five configurations, from
+    ``"B=64,Hq=16,Hkv=8,D=256,L=2048,part=512"``: every sequence at length L,
+    a seeded shuffled pool of exactly the needed blocks. Keys: B, Hq, Hkv, D,
+    Dv (default D), L, bs (16), part (split-K tokens, 0 = one partition),
+    seed (7), dtype (bf16|f16|f32), kv (native|fp8), layout (NHD|HND)."""
+    vals = {"bs": 16, "part": 0, "seed": 7, "dtype": "bf16", "kv": "native", "layout": "NHD"}
+    for item in spec.split(","):
+        key, _, raw = item.partition("=")
+        key = key.strip()
+        if key not in _SHAPE_KEYS:
+            raise ValueError(f"unknown shape key {key!r} (keys: {', '.join(_SHAPE_KEYS)})")
+        vals[key] = _SHAPE_KEYS[key](raw.strip())
+    for key in ("B", "Hq", "Hkv", "D", "L"):
+        if key not in vals:
+            raise ValueError(f"shape needs {key}")
+    d, dv = vals["D"], vals.get("Dv", vals["D"])
+    name = (f"shape_{vals['dtype']}_{vals['kv']}_{vals['layout'].lower()}_b{vals['B']}_h{vals['Hq']}x{vals['Hkv']}"
+            f"_d{d}_l{vals['L']}_p{vals['part']}")
+    return make_case(
+        name=name, dtype=_DTYPES[vals["dtype"]], sequences=vals["B"], query_heads=vals["Hq"],
+        kv_heads=vals["Hkv"], head_size=d, value_head_size=dv, block_size=vals["bs"],
+        lengths=[vals["L"]] * vals["B"], seed=vals["seed"], device=device, cache_encoding=vals["kv"],
+        layout=vals["layout"], partition_tokens=vals["part"],
+    )
+
+
 def run_case(case: DecodeCase, *, output=None, lse=None, workspace=None, return_lse=False):
     """One call of the hot path for a case (extended entry point)."""
     from .ops import paged_decode_attention_extended

@@ -436,6 +436,9 @@ def main() -> int:
                     help="decode: paged decode attention (the metric); rope: fused RoPE + paged-KV write")
     ap.add_argument("--rope-tokens", type=int, default=32768)
     ap.add_argument("--rope-cache", choices=["fp8", "native"], default="fp8")
+    ap.add_argument("--shape", default=None,
+                    help="a decode workload other than the five configurations, e.g. "
+                         "'B=64,Hq=16,Hkv=8,D=256,L=2048,part=512' (see workloads.shape_case); not the metric")
     ap.add_argument("--probe", choices=["read", "copy", "gather"], default=None,
                     help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
@@ -470,8 +473,12 @@ def main() -> int:
         return bench_reference_sweep(dev, args.sweep_path)
     if args.op == "rope":
         return bench_rope(args, dev)
-    log(f"[bench] building config {args.config} inputs")
-    case = workloads.config(args.config, dev, layout=args.layout)
+    if args.shape:
+        log(f"[bench] building shape {args.shape}")
+        case = workloads.shape_case(args.shape, dev)
+    else:
+        log(f"[bench] building config {args.config} inputs")
+        case = workloads.config(args.config, dev, layout=args.layout)
     if args.partition is not None:
         case.partition_tokens = args.partition
     out = torch.empty((case.sequences, case.query_heads, case.value_head_size), device=dev, dtype=case.dtype)
@@ -586,11 +593,14 @@ def main() -> int:
     kernel_name = {"mfma-stream": "decode_stream_kernel", "mfma": "decode_mfma_kernel"}.get(family,
                                                                                           "decode_vector_kernel")
     if family == "mfma-stream":
-        # the library's launch rule: grouped single-wave items when the grid fills the chip
-        # (>= 4096 work items)
+        # the library's launch rule: grouped single-wave items for >= 4096 work items, or >= 1024
+        # with partitions of 8+ steps of 16 tokens (head size 256: >= 4096 only); none for groups
+        # of more than 16 query heads
         pt = case.partition_tokens or case.max_sequence_length
         items = -(-case.max_sequence_length // pt) * case.kv_heads * case.sequences
-        if items >= 4096:
+        steps = -(-pt // 16)
+        grouped = items >= 4096 or (items >= 1024 and steps >= 8 and case.head_size != 256)
+        if grouped and case.query_heads // case.kv_heads <= 16:
             kernel_name = "decode_stream_group_kernel"
 
     cpu = None

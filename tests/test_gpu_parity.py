@@ -334,6 +334,22 @@ def test_stream_kernel_head_size_256(dtype, layout, shape, partition_tokens):
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_size,encoding,layout", [(128, "native", "NHD"), (128, "fp8", "HND"), (64, "native", "NHD")])
+def test_stream_kernel_grouped_mid_grid(dtype, head_size, encoding, layout):
+    """1024-4095 work items with partitions of 8+ steps: four adjacent-head
+    items per workgroup (16 sequences x 8 KV heads x 8 partitions)."""
+    lengths = [2048 - 61 * i for i in range(16)]
+    shape = (16, 32, 8, head_size, head_size, 16, lengths)
+    case = case_from(shape, dtype, seed=79, cache_encoding=encoding, layout=layout, partition_tokens=256)
+    out, lse = workloads.run_case(case, return_lse=True)
+    torch.cuda.synchronize()
+    subset = [0, 7, 15]
+    expected, want_lse = oracle_expected(case, subset)
+    assert_parity(out[subset], expected, dtype, f"grouped mid grid d{head_size} {encoding} {layout}")
+    np.testing.assert_allclose(lse[subset].cpu().numpy(), want_lse, **LSE_TOL)
+
+
 def test_config1_f32_plumbing_full():
     case = workloads.config(1, DEV)
     out, lse = workloads.run_case(case, return_lse=True)
