@@ -1161,10 +1161,11 @@ constexpr int kStreamStagesFp8 = 2;
 // (512-byte rows, two per DMA instruction).
 template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static_assert(kD == kDim || (kD == 64 && !kFp8) || (kD == 256 && !kFp8 && kHT == 1),
-                "head size 128; 64 or 256 (one head tile) with a 16-bit cache");
+  static_assert(kD == kDim || (kD == 64 && !kFp8) || (kD == 256 && kHT == 1),
+                "head size 128; 64 with a 16-bit cache; 256 with one head tile");
   static constexpr bool kNarrow = kD == 64;                  // 16-bit rows of 128 bytes
-  static constexpr bool kWide = kD == 256;                   // 16-bit rows of 512 bytes
+  static constexpr bool kWide = kD == 256 && !kFp8;          // 16-bit rows of 512 bytes
+  static constexpr bool kF8Wide = kD == 256 && kFp8;         // FP8 rows of 256 bytes
   static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
   static constexpr int kDt = kD / 16;         // 16-dim PV tiles
   static constexpr int kKc = kD / 32;         // 32-dim QK operand chunks
@@ -1175,12 +1176,12 @@ struct StreamDecoder {
   // in place. FP8: kStages stages of [K bytes 2 KiB | V bytes 2 KiB], then
   // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
   static constexpr int kStages = kFp8 ? kStreamStagesFp8 : kStreamStages;
-  static constexpr uint32_t kF8TileBytes = kStep * kDim;  // 2 KiB
+  static constexpr uint32_t kF8TileBytes = kStep * kD;  // FP8 bytes of one tensor's step
   static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kStep * kPitch;
   static constexpr uint32_t kVOff = kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
-  static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStepTileBytes : 0);
-  static constexpr int kDmaPerStep = kFp8 || kNarrow ? 4 : kWide ? 16 : 8;
+  static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStep * kPitch : 0);
+  static constexpr int kDmaPerStep = kWide ? 16 : kF8Wide ? 8 : kFp8 || kNarrow ? 4 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -1194,7 +1195,7 @@ struct StreamDecoder {
   uint32_t k_voff[4];  // 16-bit: lane's K DMA offset for rows 4i..4i+3
   uint32_t v_voff[2];  // 16-bit: lane's V DMA offset for even / odd 4-row groups
   uint32_t f8_k_voff[2], f8_v_voff[2];  // FP8: lane's K / V DMA offsets, rows 8i .. 8i + 7
-  uint32_t w_voff[kWide ? 16 : 1];      // head size 256: K offsets (rows 2i, 2i + 1), then V
+  uint32_t w_voff[kWide ? 16 : kF8Wide ? 8 : 1];  // head size 256: K offsets, then V
   float sl2;
 
   vec8 qb[kHT][kKc];
@@ -1226,7 +1227,18 @@ struct StreamDecoder {
   // instruction, chunk L of row r at L ^ ((r >> 1) & 7), which keeps the K
   // operand reads and the V conversion reads bank-conflict free.
   __device__ __forceinline__ void init_offsets() {
-    if constexpr (kWide) {
+    if constexpr (kF8Wide) {
+      // FP8 rows of 256 bytes, four per instruction: K chunk L of row r at
+      // L ^ (r & 15) (the 8-byte operand reads of 16 rows then cover all
+      // banks), V chunk L at L ^ ((r >> 1) & 7) as for head size 128.
+      const uint32_t row = lane >> 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t r = 4 * i + row;
+        w_voff[i] = static_cast<uint32_t>(row * kstride_p) + (((lane & 15U) ^ (r & 15U)) << 4);
+        w_voff[4 + i] = static_cast<uint32_t>(row * vstride_p) + (((lane & 15U) ^ ((r >> 1) & 7U)) << 4);
+      }
+    } else if constexpr (kWide) {
       // 512-byte rows, two per instruction: K chunk L of row r at L ^ (r & 15),
       // V chunk L at L ^ vtile_swizzle(r) (the bank pattern of 256-byte rows).
       const uint32_t row = lane >> 5;
@@ -1269,7 +1281,13 @@ struct StreamDecoder {
   __device__ __forceinline__ void issue(uint8_t* stage, uint32_t blk, uint32_t t0) const {
     const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
-    if constexpr (kWide) {
+    if constexpr (kF8Wide) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(w_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        vm_load16_lds_sv(w_voff[4 + i], vb + 4 * i * vstride_p, stage + kF8TileBytes + i * 1024);
+    } else if constexpr (kWide) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) vm_load16_lds_sv(w_voff[i], kb + 2 * i * kstride_p, stage + i * 1024);
 #pragma unroll
@@ -1303,8 +1321,9 @@ struct StreamDecoder {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ ((c >> 1) & 7U);
       return *reinterpret_cast<const vec8*>(stage + c * kPitch + chunk * 16);
     } else if (kFp8) {
-      const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ ((c >> 1) & 7U);
-      const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kDim + chunk * 16 + ((kc ^ g) & 1U) * 8);
+      const uint32_t swz = kF8Wide ? (c & 15U) : ((c >> 1) & 7U);
+      const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ swz;
+      const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kD + chunk * 16 + ((kc ^ g) & 1U) * 8);
       return Ops::from_fp8(w.x, w.y);
     } else {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ c;
@@ -1325,24 +1344,25 @@ struct StreamDecoder {
   }
 
   // FP8 V bytes of a stage -> the wave's swizzled 16-bit V tile: lane
-  // handles 32 bytes of token lane >> 2 (rows past the sequence end become
-  // zero).
+  // handles kD / 4 bytes of token lane >> 2 (rows past the sequence end
+  // become zero).
   __device__ __forceinline__ void stage_v_fp8(const uint8_t* stage, uint8_t* tile, uint32_t t0) const {
+    constexpr uint32_t kLaneChunks = kD / 64;  // 16-byte FP8 chunks per lane
     const uint32_t t = lane >> 2;
     const bool live = t0 + t < len;
-    const uint8_t* vrow = stage + kF8TileBytes + t * kDim;
+    const uint8_t* vrow = stage + kF8TileBytes + t * kD;
     const uint32_t odd = lane & 1U;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t lc = (lane & 3U) * 2 + h;  // logical 16-byte chunk of the FP8 row
+    for (uint32_t h = 0; h < kLaneChunks; ++h) {
+      const uint32_t lc = (lane & 3U) * kLaneChunks + h;  // logical 16-byte chunk of the FP8 row
       const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ ((t >> 1) & 7U)) << 4));
       const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
       // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each); odd lanes store the
       // upper one first so that each store instruction spans all banks.
       const vec8 lo = Ops::from_fp8(w[0], w[1]), hi = Ops::from_fp8(w[2], w[3]);
       const uint32_t ch = lc * 2;
-      *reinterpret_cast<vec8*>(tile + vtile_off(t, ch + odd)) = odd ? hi : lo;
-      *reinterpret_cast<vec8*>(tile + vtile_off(t, ch + 1 - odd)) = odd ? lo : hi;
+      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + odd)) = odd ? hi : lo;
+      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + 1 - odd)) = odd ? lo : hi;
     }
   }
 
@@ -2327,11 +2347,11 @@ bool narrow_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, u
          value_head_size == 64 && query_heads / kv_heads <= 32 && is_pow2(block_size) && block_size >= kStep;
 }
 
-// Head size 256 with a 16-bit cache: as head size 64, with at most 16 query
-// heads per KV head (one head tile per wave).
+// Head size 256 with a 16-bit or FP8 cache: as head size 64, with at most 16
+// query heads per KV head (one head tile per wave).
 bool wide_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
                 uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
-  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE && head_size == 256 &&
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding <= LOOM_HIP_KV_CACHE_FP8_E4M3 && head_size == 256 &&
          value_head_size == 256 && query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
 }
 
@@ -2341,9 +2361,10 @@ bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
       !wide_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
                   p.block_size))
     return false;
+  const uint64_t es = cache_elem_size(p);
   const uint64_t strides[] = {p.k_block, p.k_page, p.k_head, p.v_block, p.v_page, p.v_head};
   for (uint64_t st : strides) {
-    if ((st * 2) % 16 != 0) return false;
+    if ((st * es) % 16 != 0) return false;
   }
   return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) && stream_eligible(p, parts, group);
 }
@@ -2464,11 +2485,14 @@ int run_typed(const Problem& p, hipStream_t stream) {
         // 4 items per CU (measured: 1024-2048 items ran 11-15% faster as
         // one wave per item; 128 items 1.6x slower).
         if (grid >= 4096) {
-          status = launch_stream_group<QE, false, 256, 2>(args, grid, stream);
+          status = fp8 ? launch_stream_group<QE, true, 256, 2>(args, grid, stream)
+                       : launch_stream_group<QE, false, 256, 2>(args, grid, stream);
         } else if (grid >= 1024 || steps < 8) {
-          status = launch_stream<QE, false, 1, 1, 256>(args, grid, stream);
+          status = fp8 ? launch_stream<QE, true, 1, 1, 256>(args, grid, stream)
+                       : launch_stream<QE, false, 1, 1, 256>(args, grid, stream);
         } else {
-          status = launch_stream<QE, false, 4, 1, 256>(args, grid, stream);
+          status = fp8 ? launch_stream<QE, true, 4, 1, 256>(args, grid, stream)
+                       : launch_stream<QE, false, 4, 1, 256>(args, grid, stream);
         }
       } else if (group > 16) {
         status = launch_stream<QE, false, 1, 2, 64>(args, grid, stream);

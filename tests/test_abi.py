@@ -191,6 +191,8 @@ def test_capability_query():
     assert (s, fam) == (0, "vector")  # FP8 cache at head size 64: general kernel
     s, reason, fam = ops.supports(2, 0, 4, 16, 8, 256, 256, 64, 16, 16, 256, 0.0625)
     assert (s, fam) == (0, "mfma-stream")  # head size 256, 16-bit cache: 512-byte rows
+    s, reason, fam = ops.supports(2, 1, 4, 16, 8, 256, 256, 64, 16, 16, 256, 0.0625)
+    assert (s, fam) == (0, "mfma-stream")  # head size 256, FP8 cache: 256-byte rows
     s, reason, fam = ops.supports(2, 0, 4, 32, 1, 256, 256, 64, 16, 16, 256, 0.0625)
     assert (s, fam) == (0, "vector")  # head size 256 takes one head tile: groups up to 16
     s, reason, fam = ops.supports(2, 1, 128, 64, 8, 128, 128, 32768, 16, 256, 4096, 0.088)

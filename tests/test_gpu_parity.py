@@ -313,6 +313,7 @@ def test_stream_kernel_head_size_64(dtype, layout, shape, partition_tokens):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("encoding", ["native", "fp8"])
 @pytest.mark.parametrize("layout", ["NHD", "HND"])
 @pytest.mark.parametrize("shape,partition_tokens", [
     ((4, 16, 8, 256, 256, 16, [700, 1, 33, 1500]), 512),   # split over 4 waves, partial last steps
@@ -320,17 +321,20 @@ def test_stream_kernel_head_size_64(dtype, layout, shape, partition_tokens):
     ((2, 32, 2, 256, 256, 16, [400, 129]), 0),              # single partition, 16 heads per KV head
     ((128, 8, 4, 256, 256, 16, [200 - (i % 29) for i in range(128)]), 32),  # >= 4096 items: grouped launch
 ])
-def test_stream_kernel_head_size_256(dtype, layout, shape, partition_tokens):
-    """Head size 256 with a 16-bit cache on the streaming kernel (512-byte rows)."""
+def test_stream_kernel_head_size_256(dtype, encoding, layout, shape, partition_tokens):
+    """Head size 256 on the streaming kernel: 16-bit cache (512-byte rows) or
+    FP8 cache (256-byte rows converted in LDS)."""
     B, Hq, Hkv, D, Dv, bs, lengths = shape
-    case = case_from(shape, dtype, seed=73, layout=layout, partition_tokens=partition_tokens)
-    _, _, fam = ops.supports(2, 0, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
+    case = case_from(shape, dtype, seed=73, layout=layout, partition_tokens=partition_tokens,
+                     cache_encoding=encoding)
+    enc = 1 if encoding == "fp8" else 0
+    _, _, fam = ops.supports(2, enc, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
                              case.max_sequence_length, case.scale)
     assert fam == "mfma-stream"
     out, lse = workloads.run_case(case, return_lse=True)
     torch.cuda.synchronize()
     expected, want_lse = oracle_expected(case)
-    assert_parity(out, expected, dtype, f"d256 {shape[:6]} part{partition_tokens} {layout}")
+    assert_parity(out, expected, dtype, f"d256 {shape[:6]} part{partition_tokens} {encoding} {layout}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
