@@ -1155,15 +1155,16 @@ constexpr int kStreamStagesFp8 = 2;
 
 // kHT: 16-query-head tiles per wave (1, or 2 for groups of 17-32 heads). The
 // tiles share each step's K operand fetches and V transposed reads.
-// kD: head size (= value head size): 128; 64 for 16-bit caches, whose
-// 128-byte rows then take the FP8 path's DMA geometry (eight rows per
-// instruction) without a conversion; 256 for 16-bit caches and one head tile
-// (512-byte rows, two per DMA instruction).
+// kD: head size (= value head size): 128; 64, where 16-bit rows of 128 bytes
+// take the FP8 path's DMA geometry (eight rows per instruction) without a
+// conversion and FP8 rows of 64 bytes come sixteen per instruction; or 256
+// with one head tile (16-bit rows of 512 bytes two per instruction, FP8 rows
+// of 256 bytes four per instruction).
 template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static_assert(kD == kDim || (kD == 64 && !kFp8) || (kD == 256 && kHT == 1),
-                "head size 128; 64 with a 16-bit cache; 256 with one head tile");
-  static constexpr bool kNarrow = kD == 64;                  // 16-bit rows of 128 bytes
+  static_assert(kD == kDim || kD == 64 || (kD == 256 && kHT == 1), "head size 64, 128, or 256 with one head tile");
+  static constexpr bool kNarrow = kD == 64 && !kFp8;         // 16-bit rows of 128 bytes
+  static constexpr bool kF8Narrow = kD == 64 && kFp8;        // FP8 rows of 64 bytes
   static constexpr bool kWide = kD == 256 && !kFp8;          // 16-bit rows of 512 bytes
   static constexpr bool kF8Wide = kD == 256 && kFp8;         // FP8 rows of 256 bytes
   static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
@@ -1181,7 +1182,7 @@ struct StreamDecoder {
   static constexpr uint32_t kVOff = kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
   static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStep * kPitch : 0);
-  static constexpr int kDmaPerStep = kWide ? 16 : kF8Wide ? 8 : kFp8 || kNarrow ? 4 : 8;
+  static constexpr int kDmaPerStep = kWide ? 16 : kF8Wide ? 8 : kF8Narrow ? 2 : kFp8 || kNarrow ? 4 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -1227,7 +1228,15 @@ struct StreamDecoder {
   // instruction, chunk L of row r at L ^ ((r >> 1) & 7), which keeps the K
   // operand reads and the V conversion reads bank-conflict free.
   __device__ __forceinline__ void init_offsets() {
-    if constexpr (kF8Wide) {
+    if constexpr (kF8Narrow) {
+      // FP8 rows of 64 bytes, all 16 rows of a step in one instruction: chunk
+      // L of row r at L ^ ((r >> 2) & 3), so the rows sharing a 256-byte bank
+      // window hold their chunks at distinct offsets.
+      const uint32_t row = lane >> 2;
+      const uint32_t chunk = ((lane & 3U) ^ ((row >> 2) & 3U)) << 4;
+      f8_k_voff[0] = static_cast<uint32_t>(row * kstride_p) + chunk;
+      f8_v_voff[0] = static_cast<uint32_t>(row * vstride_p) + chunk;
+    } else if constexpr (kF8Wide) {
       // FP8 rows of 256 bytes, four per instruction: K chunk L of row r at
       // L ^ (r & 15) (the 8-byte operand reads of 16 rows then cover all
       // banks), V chunk L at L ^ ((r >> 1) & 7) as for head size 128.
@@ -1281,7 +1290,10 @@ struct StreamDecoder {
   __device__ __forceinline__ void issue(uint8_t* stage, uint32_t blk, uint32_t t0) const {
     const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
-    if constexpr (kF8Wide) {
+    if constexpr (kF8Narrow) {
+      vm_load16_lds_sv(f8_k_voff[0], kb, stage);
+      vm_load16_lds_sv(f8_v_voff[0], vb, stage + kF8TileBytes);
+    } else if constexpr (kF8Wide) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) vm_load16_lds_sv(w_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
 #pragma unroll
@@ -1321,7 +1333,7 @@ struct StreamDecoder {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ ((c >> 1) & 7U);
       return *reinterpret_cast<const vec8*>(stage + c * kPitch + chunk * 16);
     } else if (kFp8) {
-      const uint32_t swz = kF8Wide ? (c & 15U) : ((c >> 1) & 7U);
+      const uint32_t swz = kF8Wide ? (c & 15U) : kF8Narrow ? ((c >> 2) & 3U) : ((c >> 1) & 7U);
       const uint32_t chunk = ((static_cast<uint32_t>(kc) >> 1) * 4 + g) ^ swz;
       const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kD + chunk * 16 + ((kc ^ g) & 1U) * 8);
       return Ops::from_fp8(w.x, w.y);
@@ -1355,7 +1367,8 @@ struct StreamDecoder {
 #pragma unroll
     for (uint32_t h = 0; h < kLaneChunks; ++h) {
       const uint32_t lc = (lane & 3U) * kLaneChunks + h;  // logical 16-byte chunk of the FP8 row
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ ((t >> 1) & 7U)) << 4));
+      const uint32_t swz = kF8Narrow ? ((t >> 2) & 3U) : ((t >> 1) & 7U);
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ swz) << 4));
       const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
       // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each); odd lanes store the
       // upper one first so that each store instruction spans all banks.
@@ -2338,12 +2351,12 @@ bool stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   return 15 * p.k_page * es + 256 < limit && 15 * p.v_page * es + 256 < limit;
 }
 
-// Head size 64 with a 16-bit cache on the streaming kernel: 16-bit queries,
-// native cache, D = Dv = 64, power-of-two blocks, 16-byte aligned bases and
-// strides, and the streaming kernel's own step and offset conditions.
+// Head size 64 on the streaming kernel: 16-bit queries, native or FP8 cache,
+// D = Dv = 64, power-of-two blocks, 16-byte aligned bases and strides, and the
+// streaming kernel's own step and offset conditions.
 bool narrow_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
                   uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
-  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE && head_size == 64 &&
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding <= LOOM_HIP_KV_CACHE_FP8_E4M3 && head_size == 64 &&
          value_head_size == 64 && query_heads / kv_heads <= 32 && is_pow2(block_size) && block_size >= kStep;
 }
 
@@ -2472,8 +2485,8 @@ int run_typed(const Problem& p, hipStream_t stream) {
   }
   if (use_narrow) {
     if constexpr (!std::is_same<QE, F32Elem>::value) {
-      // Head size 64 or 256, 16-bit cache: the streaming kernel with 128- or
-      // 512-byte rows, in the launch shapes of the head-size-128 path below.
+      // Head size 64 or 256, native or FP8 cache: the streaming kernel, in the
+      // launch shapes of the head-size-128 path below.
       const uint64_t grid = parts * p.kv_heads * static_cast<uint64_t>(p.sequences);
       if (grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
         return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
@@ -2495,13 +2508,17 @@ int run_typed(const Problem& p, hipStream_t stream) {
                        : launch_stream<QE, false, 4, 1, 256>(args, grid, stream);
         }
       } else if (group > 16) {
-        status = launch_stream<QE, false, 1, 2, 64>(args, grid, stream);
+        status = fp8 ? launch_stream<QE, true, 1, 2, 64>(args, grid, stream)
+                     : launch_stream<QE, false, 1, 2, 64>(args, grid, stream);
       } else if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
-        status = launch_stream_group<QE, false, 64>(args, grid, stream);
+        status = fp8 ? launch_stream_group<QE, true, 64>(args, grid, stream)
+                     : launch_stream_group<QE, false, 64>(args, grid, stream);
       } else if (steps < 8) {
-        status = launch_stream<QE, false, 1, 1, 64>(args, grid, stream);
+        status = fp8 ? launch_stream<QE, true, 1, 1, 64>(args, grid, stream)
+                     : launch_stream<QE, false, 1, 1, 64>(args, grid, stream);
       } else {
-        status = launch_stream<QE, false, 4, 1, 64>(args, grid, stream);
+        status = fp8 ? launch_stream<QE, true, 4, 1, 64>(args, grid, stream)
+                     : launch_stream<QE, false, 4, 1, 64>(args, grid, stream);
       }
     }
   } else if (use_mfma) {

@@ -290,6 +290,7 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("encoding", ["native", "fp8"])
 @pytest.mark.parametrize("layout", ["NHD", "HND"])
 @pytest.mark.parametrize("shape,partition_tokens", [
     ((4, 32, 8, 64, 64, 16, [700, 1, 33, 2050]), 512),   # split over 4 waves, partial last steps
@@ -298,17 +299,20 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
     ((3, 32, 1, 64, 64, 16, [1100, 1, 530]), 512),       # MQA group of 32: two head tiles per wave
     ((256, 16, 8, 64, 64, 16, [300 - (i % 37) for i in range(256)]), 128),  # >= 4096 items: grouped launch
 ])
-def test_stream_kernel_head_size_64(dtype, layout, shape, partition_tokens):
-    """Head size 64 with a 16-bit cache on the streaming kernel (128-byte rows)."""
+def test_stream_kernel_head_size_64(dtype, encoding, layout, shape, partition_tokens):
+    """Head size 64 on the streaming kernel: 16-bit cache (128-byte rows) or
+    FP8 cache (64-byte rows converted in LDS)."""
     B, Hq, Hkv, D, Dv, bs, lengths = shape
-    case = case_from(shape, dtype, seed=71, layout=layout, partition_tokens=partition_tokens)
-    _, _, fam = ops.supports(2, 0, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
+    case = case_from(shape, dtype, seed=71, layout=layout, partition_tokens=partition_tokens,
+                     cache_encoding=encoding)
+    enc = 1 if encoding == "fp8" else 0
+    _, _, fam = ops.supports(2, enc, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
                              case.max_sequence_length, case.scale)
     assert fam == "mfma-stream"
     out, lse = workloads.run_case(case, return_lse=True)
     torch.cuda.synchronize()
     expected, want_lse = oracle_expected(case)
-    assert_parity(out, expected, dtype, f"d64 {shape[:6]} part{partition_tokens} {layout}")
+    assert_parity(out, expected, dtype, f"d64 {shape[:6]} part{partition_tokens} {encoding} {layout}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
