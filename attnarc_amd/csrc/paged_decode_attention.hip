@@ -8,12 +8,13 @@
 //
 // Kernels
 //   decode_stream_kernel / decode_stream_group_kernel
-//                        the main path: 16-bit query, D = Dv = 128 (native or
-//                        FP8 E4M3FN cache) or 64 (native 16-bit cache), up
-//                        to 32 query heads per KV head, power-of-two blocks
-//                        >= 16. One wave per (sequence, partition, KV head)
-//                        item streams 16-token steps: K and V rows go to LDS
-//                        by DMA (XOR-swizzled), QK^T and PV run on MFMA with
+//                        the main path: 16-bit query, D = Dv = 64, 128 or 256
+//                        (native or FP8 E4M3FN cache) or 96 (native), up to
+//                        32 query heads per KV head (16 at 96 and 256),
+//                        power-of-two blocks >= 16. One wave per (sequence,
+//                        partition, KV head) item streams 16-token steps: K
+//                        and V rows go to LDS by DMA (swizzled), QK^T and PV
+//                        run on MFMA with
 //                        the group's heads as the N dimension. Full grids
 //                        put four adjacent-head items in one workgroup.
 //   decode_mfma_kernel   the same head layout with 32-token chunks and K in
@@ -1162,11 +1163,31 @@ constexpr int kStreamStagesFp8 = 2;
 // of 256 bytes four per instruction).
 template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static_assert(kD == kDim || kD == 64 || (kD == 256 && kHT == 1), "head size 64, 128, or 256 with one head tile");
+  static_assert(kD == kDim || kD == 64 || (kD == 256 && kHT == 1) || (kD == 96 && kHT == 1 && !kFp8),
+                "head size 64, 128, 256 with one head tile, or 96 with one head tile and a 16-bit cache");
   static constexpr bool kNarrow = kD == 64 && !kFp8;         // 16-bit rows of 128 bytes
   static constexpr bool kF8Narrow = kD == 64 && kFp8;        // FP8 rows of 64 bytes
   static constexpr bool kWide = kD == 256 && !kFp8;          // 16-bit rows of 512 bytes
   static constexpr bool kF8Wide = kD == 256 && kFp8;         // FP8 rows of 256 bytes
+  // Head size 96, 16-bit: rows of 12 chunks (192 bytes). Lanes map to chunks
+  // by flat index (16 rows x 12 chunks = 3 DMA instructions per tensor), so a
+  // stage holds rows at a 192-byte pitch; a row's chunks are rotated by
+  // 3 (r >> 2) (mod 12), which puts the four rows that share a 256-byte bank
+  // window at distinct chunk offsets.
+  static constexpr bool kRot = kD == 96;
+  static constexpr uint32_t kRowChunks = kD / 8;
+  static constexpr int kRotDma = kD / 32;  // DMA instructions per tensor per step
+  static __device__ __forceinline__ uint32_t rot_slot(uint32_t r, uint32_t chunk) {
+    return (chunk + 3U * (r >> 2)) % kRowChunks;
+  }
+  // Byte offset of 16-byte chunk ch of row t in the 16-bit V tile.
+  static __device__ __forceinline__ uint32_t vt_off(uint32_t t, uint32_t ch) {
+    if constexpr (kRot) {
+      return t * kPitch + (rot_slot(t, ch) << 4);
+    } else {
+      return vtile_off<kD * 2>(t, ch);
+    }
+  }
   static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
   static constexpr int kDt = kD / 16;         // 16-dim PV tiles
   static constexpr int kKc = kD / 32;         // 32-dim QK operand chunks
@@ -1182,7 +1203,7 @@ struct StreamDecoder {
   static constexpr uint32_t kVOff = kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
   static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStep * kPitch : 0);
-  static constexpr int kDmaPerStep = kWide ? 16 : kF8Wide ? 8 : kF8Narrow ? 2 : kFp8 || kNarrow ? 4 : 8;
+  static constexpr int kDmaPerStep = kRot ? 2 * kRotDma : kWide ? 16 : kF8Wide ? 8 : kF8Narrow ? 2 : kFp8 || kNarrow ? 4 : 8;
   static constexpr uint32_t kElem = kFp8 ? 1 : 2;
 
   const DecodeArgs& a;
@@ -1196,7 +1217,7 @@ struct StreamDecoder {
   uint32_t k_voff[4];  // 16-bit: lane's K DMA offset for rows 4i..4i+3
   uint32_t v_voff[2];  // 16-bit: lane's V DMA offset for even / odd 4-row groups
   uint32_t f8_k_voff[2], f8_v_voff[2];  // FP8: lane's K / V DMA offsets, rows 8i .. 8i + 7
-  uint32_t w_voff[kWide ? 16 : kF8Wide ? 8 : 1];  // head size 256: K offsets, then V
+  uint32_t w_voff[kWide ? 16 : kF8Wide ? 8 : kRot ? 2 * kRotDma : 1];  // head size 256 / 96: K offsets, then V
   float sl2;
 
   vec8 qb[kHT][kKc];
@@ -1228,7 +1249,18 @@ struct StreamDecoder {
   // instruction, chunk L of row r at L ^ ((r >> 1) & 7), which keeps the K
   // operand reads and the V conversion reads bank-conflict free.
   __device__ __forceinline__ void init_offsets() {
-    if constexpr (kF8Narrow) {
+    if constexpr (kRot) {
+      // Lane l of instruction i fills LDS chunk 64 i + l = (row, slot); it
+      // loads the row's logical chunk whose rotated slot that is.
+#pragma unroll
+      for (int i = 0; i < kRotDma; ++i) {
+        const uint32_t idx = 64U * i + lane;
+        const uint32_t r = idx / kRowChunks, slot = idx % kRowChunks;
+        const uint32_t logical = (slot + kRowChunks - (3U * (r >> 2)) % kRowChunks) % kRowChunks;
+        w_voff[i] = static_cast<uint32_t>(r * kstride_p) + (logical << 4);
+        w_voff[kRotDma + i] = static_cast<uint32_t>(r * vstride_p) + (logical << 4);
+      }
+    } else if constexpr (kF8Narrow) {
       // FP8 rows of 64 bytes, all 16 rows of a step in one instruction: chunk
       // L of row r at L ^ ((r >> 2) & 3), so the rows sharing a 256-byte bank
       // window hold their chunks at distinct offsets.
@@ -1290,7 +1322,12 @@ struct StreamDecoder {
   __device__ __forceinline__ void issue(uint8_t* stage, uint32_t blk, uint32_t t0) const {
     const uint64_t kb = row_base(kbase, kstride_b, kstride_p, blk, t0);
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
-    if constexpr (kF8Narrow) {
+    if constexpr (kRot) {
+#pragma unroll
+      for (int i = 0; i < kRotDma; ++i) vm_load16_lds_sv(w_voff[i], kb, stage + i * 1024);
+#pragma unroll
+      for (int i = 0; i < kRotDma; ++i) vm_load16_lds_sv(w_voff[kRotDma + i], vb, stage + kVOff + i * 1024);
+    } else if constexpr (kF8Narrow) {
       vm_load16_lds_sv(f8_k_voff[0], kb, stage);
       vm_load16_lds_sv(f8_v_voff[0], vb, stage + kF8TileBytes);
     } else if constexpr (kF8Wide) {
@@ -1329,7 +1366,10 @@ struct StreamDecoder {
   // dims); the half depends on g so that the two lane groups served together
   // read different banks.
   __device__ __forceinline__ vec8 k_operand(const uint8_t* stage, int kc) const {
-    if (kNarrow) {
+    if constexpr (kRot) {
+      const uint32_t slot = rot_slot(c, static_cast<uint32_t>(kc) * 4 + g);
+      return *reinterpret_cast<const vec8*>(stage + c * kPitch + slot * 16);
+    } else if (kNarrow) {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ ((c >> 1) & 7U);
       return *reinterpret_cast<const vec8*>(stage + c * kPitch + chunk * 16);
     } else if (kFp8) {
@@ -1427,7 +1467,7 @@ struct StreamDecoder {
     lds_u8* base = (lds_u8*)tile;
 #pragma unroll
     for (uint32_t dt = 0; dt < kDt; ++dt) {
-      const uint32_t off = vtile_off<kPitch>(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
+      const uint32_t off = vt_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
       const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) acc[ht][dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb[ht], acc[ht][dt]);
@@ -2368,9 +2408,19 @@ bool wide_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uin
          value_head_size == 256 && query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
 }
 
+// Head size 96 with a 16-bit cache (192-byte rows), at most 16 query heads per
+// KV head.
+bool rot_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
+               uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE && head_size == 96 &&
+         value_head_size == 96 && query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
+}
+
 bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   if (!narrow_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
                     p.block_size) &&
+      !rot_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
+                 p.block_size) &&
       !wide_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
                   p.block_size))
     return false;
@@ -2492,7 +2542,15 @@ int run_typed(const Problem& p, hipStream_t stream) {
         return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
       args.grid_y = p.kv_heads;
       const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
-      if (p.head_size == 256) {
+      if (p.head_size == 96) {
+        if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
+          status = launch_stream_group<QE, false, 96>(args, grid, stream);
+        } else if (steps < 8) {
+          status = launch_stream<QE, false, 1, 1, 96>(args, grid, stream);
+        } else {
+          status = launch_stream<QE, false, 4, 1, 96>(args, grid, stream);
+        }
+      } else if (p.head_size == 256) {
         // 32 KiB of LDS per wave: two items per grouped workgroup, and the
         // 4-wave split (129 KiB, one workgroup per CU) only for grids under
         // 4 items per CU (measured: 1024-2048 items ran 11-15% faster as
@@ -2879,7 +2937,9 @@ int loom_hip_paged_decode_attention_supports(
                      : narrow_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
                                     block_size) ||
                                wide_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
-                                          block_size)
+                                          block_size) ||
+                               rot_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
+                                         block_size)
                          ? "mfma-stream"
                      : !mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
                          ? "vector"

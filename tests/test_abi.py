@@ -189,8 +189,12 @@ def test_capability_query():
     assert (s, fam) == (0, "mfma-stream")  # head size 64, 16-bit cache: 128-byte rows
     s, reason, fam = ops.supports(2, 1, 4, 8, 8, 64, 64, 64, 16, 16, 256, 0.125)
     assert (s, fam) == (0, "mfma-stream")  # FP8 cache at head size 64: 64-byte rows
+    s, reason, fam = ops.supports(2, 0, 4, 8, 8, 96, 96, 64, 16, 16, 256, 0.102)
+    assert (s, fam) == (0, "mfma-stream")  # head size 96, 16-bit cache: 192-byte rows
     s, reason, fam = ops.supports(2, 1, 4, 8, 8, 96, 96, 64, 16, 16, 256, 0.102)
-    assert (s, fam) == (0, "vector")  # head size 96: general kernel
+    assert (s, fam) == (0, "vector")  # FP8 cache at head size 96: general kernel
+    s, reason, fam = ops.supports(2, 0, 4, 8, 8, 80, 80, 64, 16, 16, 256, 0.11)
+    assert (s, fam) == (0, "vector")  # head size 80: general kernel
     s, reason, fam = ops.supports(2, 0, 4, 16, 8, 256, 256, 64, 16, 16, 256, 0.0625)
     assert (s, fam) == (0, "mfma-stream")  # head size 256, 16-bit cache: 512-byte rows
     s, reason, fam = ops.supports(2, 1, 4, 16, 8, 256, 256, 64, 16, 16, 256, 0.0625)
