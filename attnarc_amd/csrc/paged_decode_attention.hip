@@ -766,8 +766,12 @@ struct MfmaDecoder {
       const uint32_t ch = (lane & 7U) * 2;
       const vec8 lo = Ops::from_fp8(b.v[i][0], b.v[i][1]);
       const vec8 hi = Ops::from_fp8(b.v[i][2], b.v[i][3]);
-      *reinterpret_cast<vec8*>(tile + tile_off(t, ch)) = lo;
-      *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1)) = hi;
+      // 16-byte LDS writes are served 8 lanes at a time over 128 bytes of
+      // banks: lanes 4..7 of each eight store their upper chunk first, so the
+      // eight chunks of one store land in distinct 16-byte bank quarters.
+      const uint32_t up = (lane >> 2) & 1U;
+      *reinterpret_cast<vec8*>(tile + tile_off(t, ch + up)) = up ? hi : lo;
+      *reinterpret_cast<vec8*>(tile + tile_off(t, ch + 1 - up)) = up ? lo : hi;
     }
   }
 
@@ -1269,15 +1273,17 @@ struct StreamDecoder {
       f8_k_voff[0] = static_cast<uint32_t>(row * kstride_p) + chunk;
       f8_v_voff[0] = static_cast<uint32_t>(row * vstride_p) + chunk;
     } else if constexpr (kF8Wide) {
-      // FP8 rows of 256 bytes, four per instruction: K chunk L of row r at
-      // L ^ (r & 15) (the 8-byte operand reads of 16 rows then cover all
-      // banks), V chunk L at L ^ ((r >> 1) & 7) as for head size 128.
+      // FP8 rows of 256 bytes, four per instruction: chunk L of row r at
+      // L ^ (r & 15) in K and in V (the 8-byte K operand reads of 16 rows,
+      // and the V conversion reads of 16 rows at one chunk, then cover all
+      // banks).
       const uint32_t row = lane >> 4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t r = 4 * i + row;
-        w_voff[i] = static_cast<uint32_t>(row * kstride_p) + (((lane & 15U) ^ (r & 15U)) << 4);
-        w_voff[4 + i] = static_cast<uint32_t>(row * vstride_p) + (((lane & 15U) ^ ((r >> 1) & 7U)) << 4);
+        const uint32_t chunk = ((lane & 15U) ^ (r & 15U)) << 4;
+        w_voff[i] = static_cast<uint32_t>(row * kstride_p) + chunk;
+        w_voff[4 + i] = static_cast<uint32_t>(row * vstride_p) + chunk;
       }
     } else if constexpr (kWide) {
       // 512-byte rows, two per instruction: K chunk L of row r at L ^ (r & 15),
@@ -1395,27 +1401,32 @@ struct StreamDecoder {
     }
   }
 
-  // FP8 V bytes of a stage -> the wave's swizzled 16-bit V tile: lane
-  // handles kD / 4 bytes of token lane >> 2 (rows past the sequence end
-  // become zero).
+  // FP8 V bytes of a stage -> the wave's swizzled 16-bit V tile (rows past
+  // the sequence end become zero). Head sizes 64 and 128: lane handles kD / 4
+  // bytes of token lane >> 2; head size 256: lane handles 64 bytes of token
+  // lane & 15. 16-byte LDS reads are served 16 lanes at a time over 256 bytes
+  // of banks, 16-byte writes 8 lanes at a time over 128 bytes; the row
+  // mapping, the V swizzle and the order of each lane's two stores (the
+  // `up` lanes store the upper 16-bit chunk first) keep every read and every
+  // store free of bank conflicts.
   __device__ __forceinline__ void stage_v_fp8(const uint8_t* stage, uint8_t* tile, uint32_t t0) const {
     constexpr uint32_t kLaneChunks = kD / 64;  // 16-byte FP8 chunks per lane
-    const uint32_t t = lane >> 2;
+    const uint32_t t = kF8Wide ? (lane & 15U) : (lane >> 2);
+    const uint32_t q = kF8Wide ? (lane >> 4) : (lane & 3U);
     const bool live = t0 + t < len;
     const uint8_t* vrow = stage + kF8TileBytes + t * kD;
-    const uint32_t odd = lane & 1U;
+    const uint32_t up = kF8Wide ? ((t >> 2) & 1U) : kF8Narrow ? (lane & 1U) : ((lane >> 1) & 1U);
+    const uint32_t swz = kF8Wide ? (t & 15U) : kF8Narrow ? ((t >> 2) & 3U) : ((t >> 1) & 7U);
 #pragma unroll
     for (uint32_t h = 0; h < kLaneChunks; ++h) {
-      const uint32_t lc = (lane & 3U) * kLaneChunks + h;  // logical 16-byte chunk of the FP8 row
-      const uint32_t swz = kF8Narrow ? ((t >> 2) & 3U) : ((t >> 1) & 7U);
+      const uint32_t lc = q * kLaneChunks + h;  // logical 16-byte chunk of the FP8 row
       const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ swz) << 4));
       const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
-      // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each); odd lanes store the
-      // upper one first so that each store instruction spans all banks.
+      // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each).
       const vec8 lo = Ops::from_fp8(w[0], w[1]), hi = Ops::from_fp8(w[2], w[3]);
       const uint32_t ch = lc * 2;
-      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + odd)) = odd ? hi : lo;
-      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + 1 - odd)) = odd ? lo : hi;
+      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + up)) = up ? hi : lo;
+      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + 1 - up)) = up ? lo : hi;
     }
   }
 
@@ -1486,6 +1497,7 @@ struct StreamDecoder {
 struct WorkItem {
   uint32_t seq, part, kvh, len;
   bool valid;
+  uint32_t h0;  // first query head of the group this wave computes (0 below 33 heads)
 };
 
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane) {
@@ -1607,7 +1619,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   const uint32_t seq = item.seq;
   const uint32_t len = item.len;
   const uint32_t p0 = part * a.partition_tokens;
-  static_assert(kSplit * Dec::kWaveBytes >= kSplit * 16 * kD * sizeof(float),
+  static_assert(Dec::kWaveBytes >= 16 * (kD + 4) * sizeof(float),
                 "the cross-wave reduction reuses the stages");
 
   Dec dec(a);
@@ -1675,7 +1687,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       u32x4 qw[kHT][Dec::kKc];
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) {
-        const uint32_t h = min(ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
+        const uint32_t h = min(item.h0 + ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
         const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
                                (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kD;
 #pragma unroll
@@ -1692,7 +1704,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       }
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) {
-        const bool live = ht * 16U + dec.c < a.group;
+        const bool live = item.h0 + ht * 16U + dec.c < a.group;
 #pragma unroll
         for (int kc = 0; kc < Dec::kKc; ++kc)
           dec.qb[ht][kc] = __builtin_bit_cast(vec8, live ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
@@ -1737,7 +1749,8 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   if (kSplit == 1) {
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
-      if (ht * 16U + dec.c < a.group) store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
+      if (item.h0 + ht * 16U + dec.c < a.group)
+        store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + item.h0 + ht * 16U, part, v_scale, lt[ht]);
     }
     return;
   }
@@ -1745,7 +1758,10 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   // Several waves split the partition (one head tile): reduce through LDS.
   const uint32_t h = dec.c;
   const float l = lt[0];
-  float (*red_o)[16][kD] = reinterpret_cast<float (*)[16][kD]>(tiles);
+  // Rows padded by 16 bytes: the eight lanes of one 16-byte store then fall
+  // in distinct bank quarters.
+  constexpr uint32_t kRedPitch = kD + 4;
+  float (*red_o)[16][kRedPitch] = reinterpret_cast<float (*)[16][kRedPitch]>(tiles);
   __shared__ float red_ml[kSplit][16][2];
   __syncthreads();  // every wave is done with its V tiles
   if (dec.g == 0) {
@@ -1784,6 +1800,149 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   }
 }
 
+// Workgroup barrier after this wave's LDS operations have completed. Unlike
+// __syncthreads it leaves outstanding global loads (the DMA pipeline) alone;
+// the clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
+// Pipeline stages shared by the waves of a wide-group workgroup (16-bit: 8 KiB
+// each; FP8: 4 KiB, plus one converted V tile per wave).
+constexpr int kSharedStages = 4;
+
+// One work item of a group of 33-128 query heads: kWaves waves, wave w
+// computing heads 32 w .. 32 w + 31 with two head tiles, from a ring of K/V
+// stages that all waves share. Wave 0 issues every step's DMA. One barrier
+// per step, after wave 0's wait for the step's stage, both publishes that
+// stage and shows that every wave has finished the previous step, whose
+// stage wave 0 then refills (S - 1 steps ahead). The waves have the same
+// steps, so all of them reach every barrier.
+template <typename QE, bool kFp8, int kWaves, uint32_t kD>
+__device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
+  using Dec = StreamDecoder<QE, kFp8, 2, kD>;
+  using vec8 = typename Dec::vec8;
+  constexpr int S = kSharedStages;
+  const uint32_t kvh = item.kvh, part = item.part, seq = item.seq, len = item.len;
+  const uint32_t p0 = part * a.partition_tokens;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t h0 = wave * 32U;
+
+  Dec dec(a);
+  dec.lane = threadIdx.x & 63U;
+  dec.g = dec.lane >> 4;
+  dec.c = dec.lane & 15U;
+  dec.len = len;
+  dec.p1 = min(p0 + a.partition_tokens, len);
+  dec.last_block = (len - 1U) >> a.block_shift;
+  dec.table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
+  constexpr uint32_t es = Dec::kElem;
+  dec.kstride_b = a.k_block * es;
+  dec.vstride_b = a.v_block * es;
+  dec.kstride_p = a.k_page * es;
+  dec.vstride_p = a.v_page * es;
+  dec.kbase = reinterpret_cast<uint64_t>(a.key_cache) + static_cast<uint64_t>(kvh) * a.k_head * es;
+  dec.vbase = reinterpret_cast<uint64_t>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head * es;
+  dec.init_offsets();
+  uint8_t* vconv = tiles + S * Dec::kStageBytes + wave * (kStep * Dec::kPitch);  // FP8: this wave's 16-bit V
+
+  float k_scale = 1.0f, v_scale = 1.0f;
+  if (kFp8) {
+    k_scale = a.key_scales[kvh * a.scale_stride];
+    v_scale = a.value_scales[kvh * a.scale_stride];
+  }
+  dec.sl2 = a.score_scale_log2 * k_scale;
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    dec.m[ht] = -INFINITY;
+    dec.lsum[ht] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < Dec::kDt; ++dt) dec.acc[ht][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  const uint32_t nst = (dec.p1 - p0 + kStep - 1) / kStep;  // >= 1: the item holds tokens
+  const uint32_t t_last = p0 + (nst - 1) * kStep;
+  // nx[j]: block of the next step that wave 0 loads into stage j (steps past
+  // the item's last are clamped onto it: cache hits, keeping the issue uniform).
+  uint32_t nx[S];
+  if (wave == 0) {
+    uint32_t bk[S - 1];
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) bk[i] = dec.block_of(min(p0 + i * kStep, t_last));
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) nx[i] = dec.block_of(min(p0 + (S + i) * kStep, t_last));
+    nx[S - 1] = dec.block_of(min(p0 + (S - 1) * kStep, t_last));
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) scalar_ready(bk[i]);
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i) dec.issue(tiles + i * Dec::kStageBytes, bk[i], min(p0 + i * kStep, t_last));
+  }
+  {
+    u32x4 qw[2][Dec::kKc];
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+      const uint32_t h = min(h0 + ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
+      const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
+                             (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kD;
+#pragma unroll
+      for (int kc = 0; kc < Dec::kKc; ++kc) {
+        const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
+        vm_load16(qw[ht][kc], qrow + dim);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+#pragma unroll
+      for (int kc = 0; kc < Dec::kKc; ++kc) asm volatile("" : "+v"(qw[ht][kc]));  // loaded: the wait above was vmcnt(0)
+    }
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+      const bool live = h0 + ht * 16U + dec.c < a.group;
+#pragma unroll
+      for (int kc = 0; kc < Dec::kKc; ++kc)
+        dec.qb[ht][kc] = __builtin_bit_cast(vec8, live ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
+    }
+  }
+
+  for (uint32_t n = 0; n < nst; n += S) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      if (n + i < nst) {
+        const uint32_t t0 = p0 + (n + i) * kStep;
+        uint8_t* stage = tiles + i * Dec::kStageBytes;
+        const int j = (i + S - 1) % S;  // the stage of the previous step
+        if (wave == 0) {
+          vm_wait_dma<Dec::kDmaPerStep * (S - 2)>();  // this step's loads; S - 2 later steps stay in flight
+          if (!kFp8) dec.zero_dead_rows(stage + Dec::kVOff, t0);
+        }
+        lds_barrier();  // this step's stage is in LDS; every wave is done with the previous one
+        if (wave == 0) {
+          scalar_ready(nx[j]);
+          dec.issue(tiles + j * Dec::kStageBytes, nx[j], min(t0 + (S - 1) * kStep, t_last));
+          nx[j] = dec.block_of(min(t0 + (2 * S - 1) * kStep, t_last));
+        }
+        uint8_t* vtile = kFp8 ? vconv : stage + Dec::kVOff;
+        if (kFp8) {
+          dec.stage_v_fp8(stage, vtile, t0);
+          wave_fence_lds();
+        }
+        f32x4 sc[2];
+        dec.qk(stage, sc);
+        dec.softmax_pv(sc, t0, vtile);
+      }
+    }
+  }
+  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    float l = dec.lsum[ht];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (h0 + ht * 16U + dec.c < a.group)
+      store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + h0 + ht * 16U, part, v_scale, l);
+  }
+}
+
 template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_kernel(DecodeArgs a) {
@@ -1811,6 +1970,20 @@ void decode_stream_group_kernel(DecodeArgs a) {
   const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
   if (!item.valid) return;  // per wave: nothing below waits on the other waves
   stream_item<QE, kFp8, 1, 1, kD>(a, tiles + wave * Dec::kWaveBytes, item);
+}
+
+// Groups of 33-128 query heads: one workgroup of ceil(group / 32) waves per
+// work item (stream_item_shared), so that each K/V row is read from HBM once
+// into LDS for all of the group's heads.
+template <typename QE, bool kFp8, int kWaves, uint32_t kD = kDim>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_stream_heads_kernel(DecodeArgs a) {
+  using Dec = StreamDecoder<QE, kFp8, 2, kD>;
+  __shared__ __attribute__((aligned(16)))
+  uint8_t tiles[kSharedStages * Dec::kStageBytes + (kFp8 ? kWaves * kStep * Dec::kPitch : 0)];
+  const WorkItem item = schedule_item(a, blockIdx.x);
+  if (!item.valid) return;  // uniform across the workgroup
+  stream_item_shared<QE, kFp8, kWaves, kD>(a, tiles, item);
 }
 
 // ---------------------------------------------------------------------------
@@ -2416,6 +2589,47 @@ bool rot_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint
          value_head_size == 96 && query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
 }
 
+// Groups of 33-128 query heads at head size 64 or 128, native or FP8 cache:
+// the streaming kernel with one wave per 32 heads of the group.
+bool heads_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
+                 uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
+  const uint32_t group = query_heads / kv_heads;
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding <= LOOM_HIP_KV_CACHE_FP8_E4M3 &&
+         (head_size == 64 || head_size == kDim) && value_head_size == head_size && group > 32 && group <= 128 &&
+         is_pow2(block_size) && block_size >= kStep;
+}
+
+bool heads_stream_eligible(const Problem& p, uint64_t parts) {
+  if (!heads_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
+                   p.block_size))
+    return false;
+  const uint64_t es = cache_elem_size(p);
+  const uint64_t strides[] = {p.k_block, p.k_page, p.k_head, p.v_block, p.v_page, p.v_head};
+  for (uint64_t st : strides) {
+    if ((st * es) % 16 != 0) return false;
+  }
+  if (parts > 1 && p.partition_tokens % kStep != 0) return false;
+  const uint64_t limit = 1ULL << 31;
+  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) &&
+         15 * p.k_page * es + 256 < limit && 15 * p.v_page * es + 256 < limit;
+}
+
+template <typename QE, bool kFp8, uint32_t kD>
+int launch_stream_heads(const DecodeArgs& args, uint64_t items, uint32_t group, hipStream_t stream) {
+  using Dec = StreamDecoder<QE, kFp8, 2, kD>;
+  TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  static_assert(4 * Dec::kWaveBytes <= 64 * 1024, "four waves' stages fit in 64 KiB of LDS");
+  const dim3 grid(static_cast<uint32_t>(items));
+  if (group <= 64) {
+    hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 2, kD>), grid, dim3(128), 0, stream, args);
+  } else if (group <= 96) {
+    hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 3, kD>), grid, dim3(192), 0, stream, args);
+  } else {
+    hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 4, kD>), grid, dim3(256), 0, stream, args);
+  }
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
 bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   if (!narrow_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
                     p.block_size) &&
@@ -2528,12 +2742,27 @@ int run_typed(const Problem& p, hipStream_t stream) {
   args.score_scale_log2 = p.scale * kLog2e;
 
   int status = LOOM_HIP_SUCCESS;
-  bool use_narrow = false, use_mfma = false;
+  bool use_narrow = false, use_mfma = false, use_heads = false;
   if constexpr (!std::is_same<QE, F32Elem>::value) {
-    use_narrow = narrow_stream_eligible(p, parts, group);
-    use_mfma = !use_narrow && mfma_eligible(p);
+    use_heads = heads_stream_eligible(p, parts);
+    use_narrow = !use_heads && narrow_stream_eligible(p, parts, group);
+    use_mfma = !use_heads && !use_narrow && mfma_eligible(p);
   }
-  if (use_narrow) {
+  if (use_heads) {
+    if constexpr (!std::is_same<QE, F32Elem>::value) {
+      const uint64_t grid = parts * p.kv_heads * static_cast<uint64_t>(p.sequences);
+      if (grid > static_cast<uint64_t>(std::numeric_limits<int>::max()))
+        return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
+      args.grid_y = p.kv_heads;
+      if (p.head_size == 64) {
+        status = fp8 ? launch_stream_heads<QE, true, 64>(args, grid, group, stream)
+                     : launch_stream_heads<QE, false, 64>(args, grid, group, stream);
+      } else {
+        status = fp8 ? launch_stream_heads<QE, true, kDim>(args, grid, group, stream)
+                     : launch_stream_heads<QE, false, kDim>(args, grid, group, stream);
+      }
+    }
+  } else if (use_narrow) {
     if constexpr (!std::is_same<QE, F32Elem>::value) {
       // Head size 64 or 256, native or FP8 cache: the streaming kernel, in the
       // launch shapes of the head-size-128 path below.
@@ -2939,7 +3168,9 @@ int loom_hip_paged_decode_attention_supports(
                                wide_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
                                           block_size) ||
                                rot_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
-                                         block_size)
+                                         block_size) ||
+                               heads_shape(dtype, cache_encoding, head_size, value_head_size, query_heads, kv_heads,
+                                           block_size)
                          ? "mfma-stream"
                      : !mfma_shape(dtype, head_size, value_head_size, query_heads, kv_heads, block_size)
                          ? "vector"

@@ -600,7 +600,9 @@ def main() -> int:
         items = -(-case.max_sequence_length // pt) * case.kv_heads * case.sequences
         steps = -(-pt // 16)
         grouped = items >= 4096 or (items >= 1024 and steps >= 8 and case.head_size != 256)
-        if grouped and case.query_heads // case.kv_heads <= 16:
+        if case.query_heads // case.kv_heads > 32:
+            kernel_name = "decode_stream_heads_kernel"  # one wave per 32 heads of the group
+        elif grouped and case.query_heads // case.kv_heads <= 16:
             kernel_name = "decode_stream_group_kernel"
 
     cpu = None

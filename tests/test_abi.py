@@ -203,6 +203,14 @@ def test_capability_query():
     assert (s, fam) == (0, "vector")  # head size 256 takes one head tile: groups up to 16
     s, reason, fam = ops.supports(2, 1, 128, 64, 8, 128, 128, 32768, 16, 256, 4096, 0.088)
     assert (s, fam) == (0, "mfma-stream")
+    s, reason, fam = ops.supports(2, 1, 32, 64, 1, 128, 128, 8192, 16, 256, 4096, 0.088)
+    assert (s, fam) == (0, "mfma-stream")  # MQA group of 64: one wave per 32 heads
+    s, reason, fam = ops.supports(2, 0, 8, 71, 1, 64, 64, 8192, 16, 256, 4096, 0.125)
+    assert (s, fam) == (0, "mfma-stream")  # group of 71 at head size 64: three waves
+    s, reason, fam = ops.supports(2, 0, 8, 129, 1, 128, 128, 8192, 16, 256, 4096, 0.088)
+    assert (s, fam) == (0, "vector")  # groups above 128 heads: general kernel
+    s, reason, fam = ops.supports(2, 0, 8, 64, 1, 128, 128, 8192, 8, 512, 4096, 0.088)
+    assert (s, fam) == (0, "vector")  # wide groups need blocks of at least 16 tokens
     s, reason, fam = ops.supports(2, 0, 8, 32, 1, 128, 128, 65536, 16, 8192, 131072, 0.088)
     assert (s, fam) == (0, "mfma-stream")
     s, reason, _ = ops.supports(7, 0, 4, 8, 8, 64, 64, 64, 16, 16, 256, 0.125)
