@@ -1116,12 +1116,18 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
 constexpr uint32_t kStep = 16;
 constexpr uint32_t kStepTileBytes = kStep * kTileRowBytes;  // 4 KiB
 
-// Chunk permutation of row t in a 16-bit V tile: 2 (t & 7) for 256-byte rows
-// (head size 128), 2 (t & 3) for 128-byte rows (head size 64), so that a
-// row's chunks stay inside the row.
+// Chunk permutation of row t in a 16-bit V tile, so that a row's chunks stay
+// inside the row: 2 (t & 7) for rows of 256 bytes or more (head size 128 and
+// up); 2 (((t >> 1) & 3) ^ (t & 1)) for 128-byte rows (head size 64). The
+// transposed 8-byte reads are served 32 lanes (rows 4g .. 4g + 3 of two lane
+// groups g, eight rows) at a time over 256 bytes of banks, where rows t and
+// t + 2 share bank offsets at the 128-byte pitch: the permutation differs
+// across each such set of four rows. It also differs in bit 1 between rows
+// 2k and 2k + 1, which keeps the FP8 conversion's 16-byte stores (8 lanes,
+// two rows, 128 bytes of banks at a time) conflict-free.
 template <uint32_t kPitch>
 __host__ __device__ constexpr uint32_t vtile_swizzle(uint32_t t) {
-  return kPitch >= 256 ? (t & 7U) << 1 : (t & 3U) << 1;
+  return kPitch >= 256 ? (t & 7U) << 1 : (((t >> 1) & 3U) ^ (t & 1U)) << 1;
 }
 
 // Byte offset of 16-byte chunk ch of row t in a 16-bit V tile (256-byte
