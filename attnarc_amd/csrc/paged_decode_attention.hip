@@ -9,14 +9,17 @@
 // Kernels
 //   decode_stream_kernel / decode_stream_group_kernel
 //                        the main path: 16-bit query, D = Dv = 64, 128 or 256
-//                        (native or FP8 E4M3FN cache) or 96 (native), up to
-//                        32 query heads per KV head (16 at 96 and 256),
+//                        (native or FP8 E4M3FN cache) or 80, 96, 112 (native),
+//                        up to 32 query heads per KV head (16 at 80-112 and 256),
 //                        power-of-two blocks >= 16. One wave per (sequence,
 //                        partition, KV head) item streams 16-token steps: K
 //                        and V rows go to LDS by DMA (swizzled), QK^T and PV
 //                        run on MFMA with
 //                        the group's heads as the N dimension. Full grids
 //                        put four adjacent-head items in one workgroup.
+//   decode_stream_heads_kernel
+//                        groups of 33-128 query heads at D = 64 or 128: one
+//                        wave per 32 heads, all reading one shared LDS ring.
 //   decode_mfma_kernel   the same head layout with 32-token chunks and K in
 //                        registers, for block sizes below 16 and partitions
 //                        that are not a multiple of 16 tokens.
@@ -1173,8 +1176,9 @@ constexpr int kStreamStagesFp8 = 2;
 // of 256 bytes four per instruction).
 template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static_assert(kD == kDim || kD == 64 || (kD == 256 && kHT == 1) || (kD == 96 && kHT == 1 && !kFp8),
-                "head size 64, 128, 256 with one head tile, or 96 with one head tile and a 16-bit cache");
+  static_assert(kD == kDim || kD == 64 || (kD == 256 && kHT == 1) ||
+                    ((kD == 80 || kD == 96 || kD == 112) && kHT == 1 && !kFp8),
+                "head size 64, 128, 256 with one head tile, or 80 / 96 / 112 with one head tile and a 16-bit cache");
   static constexpr bool kNarrow = kD == 64 && !kFp8;         // 16-bit rows of 128 bytes
   static constexpr bool kF8Narrow = kD == 64 && kFp8;        // FP8 rows of 64 bytes
   static constexpr bool kWide = kD == 256 && !kFp8;          // 16-bit rows of 512 bytes
@@ -1184,9 +1188,13 @@ struct StreamDecoder {
   // stage holds rows at a 192-byte pitch; a row's chunks are rotated by
   // 3 (r >> 2) (mod 12), which puts the four rows that share a 256-byte bank
   // window at distinct chunk offsets.
-  static constexpr bool kRot = kD == 96;
+  // Head sizes 80 and 112 take the same layout: rows of 10 or 14 chunks, a
+  // tensor's step rounded up to whole DMA instructions (the spare lanes load
+  // a valid chunk into the unused tail), QK over 3 or 4 operand chunks with
+  // the chunks past the row read as zero.
+  static constexpr bool kRot = kD == 80 || kD == 96 || kD == 112;
   static constexpr uint32_t kRowChunks = kD / 8;
-  static constexpr int kRotDma = kD / 32;  // DMA instructions per tensor per step
+  static constexpr int kRotDma = (kStep * kRowChunks + 63) / 64;  // DMA instructions per tensor per step
   static __device__ __forceinline__ uint32_t rot_slot(uint32_t r, uint32_t chunk) {
     return (chunk + 3U * (r >> 2)) % kRowChunks;
   }
@@ -1200,7 +1208,7 @@ struct StreamDecoder {
   }
   static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
   static constexpr int kDt = kD / 16;         // 16-dim PV tiles
-  static constexpr int kKc = kD / 32;         // 32-dim QK operand chunks
+  static constexpr int kKc = (kD + 31) / 32;  // 32-dim QK operand chunks (the last one zero-padded)
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
@@ -1209,8 +1217,8 @@ struct StreamDecoder {
   // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
   static constexpr int kStages = kFp8 ? kStreamStagesFp8 : kStreamStages;
   static constexpr uint32_t kF8TileBytes = kStep * kD;  // FP8 bytes of one tensor's step
-  static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kStep * kPitch;
-  static constexpr uint32_t kVOff = kStep * kPitch;  // 16-bit: V within a stage
+  static constexpr uint32_t kVOff = kRot ? kRotDma * 1024 : kStep * kPitch;  // 16-bit: V within a stage
+  static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kVOff;
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
   static constexpr uint32_t kWaveBytes = kStages * kStageBytes + (kFp8 ? kStep * kPitch : 0);
   static constexpr int kDmaPerStep = kRot ? 2 * kRotDma : kWide ? 16 : kF8Wide ? 8 : kF8Narrow ? 2 : kFp8 || kNarrow ? 4 : 8;
@@ -1265,8 +1273,9 @@ struct StreamDecoder {
 #pragma unroll
       for (int i = 0; i < kRotDma; ++i) {
         const uint32_t idx = 64U * i + lane;
-        const uint32_t r = idx / kRowChunks, slot = idx % kRowChunks;
-        const uint32_t logical = (slot + kRowChunks - (3U * (r >> 2)) % kRowChunks) % kRowChunks;
+        const bool spare = idx >= kStep * kRowChunks;  // past the step's rows: reload row 15, chunk 0
+        const uint32_t r = spare ? kStep - 1 : idx / kRowChunks, slot = spare ? 0U : idx % kRowChunks;
+        const uint32_t logical = spare ? 0U : (slot + kRowChunks - (3U * (r >> 2)) % kRowChunks) % kRowChunks;
         w_voff[i] = static_cast<uint32_t>(r * kstride_p) + (logical << 4);
         w_voff[kRotDma + i] = static_cast<uint32_t>(r * vstride_p) + (logical << 4);
       }
@@ -1379,8 +1388,13 @@ struct StreamDecoder {
   // read different banks.
   __device__ __forceinline__ vec8 k_operand(const uint8_t* stage, int kc) const {
     if constexpr (kRot) {
-      const uint32_t slot = rot_slot(c, static_cast<uint32_t>(kc) * 4 + g);
-      return *reinterpret_cast<const vec8*>(stage + c * kPitch + slot * 16);
+      const uint32_t chunk = static_cast<uint32_t>(kc) * 4 + g;
+      const uint32_t slot = rot_slot(c, chunk < kRowChunks ? chunk : 0U);
+      const vec8 k = *reinterpret_cast<const vec8*>(stage + c * kPitch + slot * 16);
+      if constexpr (kRowChunks % 4 != 0) {
+        if (chunk >= kRowChunks) return vec8{};  // dims past the head size
+      }
+      return k;
     } else if (kNarrow) {
       const uint32_t chunk = (static_cast<uint32_t>(kc) * 4 + g) ^ ((c >> 1) & 7U);
       return *reinterpret_cast<const vec8*>(stage + c * kPitch + chunk * 16);
@@ -1442,9 +1456,16 @@ struct StreamDecoder {
     if (t0 + kStep <= len) return;  // uniform
     const uint32_t t = lane >> 2;   // 4 lanes per row, kPitch / 4 bytes each
     if (t0 + t >= len) {
-      u32x4* row = reinterpret_cast<u32x4*>(tile + t * kPitch + (lane & 3U) * (kPitch / 4));
+      uint8_t* part = tile + t * kPitch + (lane & 3U) * (kPitch / 4);
+      if constexpr ((kPitch / 4) % 16 == 0) {
+        u32x4* row = reinterpret_cast<u32x4*>(part);
 #pragma unroll
-      for (uint32_t i = 0; i < kPitch / 64; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
+        for (uint32_t i = 0; i < kPitch / 64; ++i) row[i] = u32x4{0U, 0U, 0U, 0U};
+      } else {  // 40- or 56-byte quarters (head sizes 80, 112): 8-byte stores
+        uint2* row = reinterpret_cast<uint2*>(part);
+#pragma unroll
+        for (uint32_t i = 0; i < kPitch / 32; ++i) row[i] = make_uint2(0U, 0U);
+      }
     }
   }
 
@@ -1699,7 +1720,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
 #pragma unroll
         for (int kc = 0; kc < Dec::kKc; ++kc) {
           const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
-          vm_load16(qw[ht][kc], qrow + dim);
+          vm_load16(qw[ht][kc], qrow + (dim < kD ? dim : 0U));  // dims past the head size are zeroed below
         }
       }
       asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
@@ -1712,8 +1733,10 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       for (int ht = 0; ht < kHT; ++ht) {
         const bool live = item.h0 + ht * 16U + dec.c < a.group;
 #pragma unroll
-        for (int kc = 0; kc < Dec::kKc; ++kc)
-          dec.qb[ht][kc] = __builtin_bit_cast(vec8, live ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
+        for (int kc = 0; kc < Dec::kKc; ++kc) {
+          const bool in_row = kFp8 || kc * 32U + dec.g * 8U < kD;
+          dec.qb[ht][kc] = __builtin_bit_cast(vec8, live && in_row ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
+        }
       }
     }
     for (uint32_t n = 0; n < my_n; n += S) {
@@ -2558,6 +2581,15 @@ int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
+// Head sizes 80, 96 and 112 (16-bit cache, one head tile): the launch shapes
+// of head size 128.
+template <typename QE, uint32_t kD>
+int launch_stream_rot(const DecodeArgs& args, uint64_t grid, uint32_t steps, hipStream_t stream) {
+  if (grid >= 4096 || (grid >= 1024 && steps >= 8)) return launch_stream_group<QE, false, kD>(args, grid, stream);
+  if (steps < 8) return launch_stream<QE, false, 1, 1, kD>(args, grid, stream);
+  return launch_stream<QE, false, 4, 1, kD>(args, grid, stream);
+}
+
 // The streaming kernel needs steps that stay inside one block (power-of-two
 // block size >= 16, partitions starting on multiples of 16), at most 32 query
 // heads per KV head (two 16-head tiles per wave), and per-lane byte offsets
@@ -2591,8 +2623,9 @@ bool wide_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uin
 // KV head.
 bool rot_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
                uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
-  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE && head_size == 96 &&
-         value_head_size == 96 && query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE &&
+         (head_size == 80 || head_size == 96 || head_size == 112) && value_head_size == head_size &&
+         query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
 }
 
 // Groups of 33-128 query heads at head size 64 or 128, native or FP8 cache:
@@ -2777,14 +2810,12 @@ int run_typed(const Problem& p, hipStream_t stream) {
         return fail(LOOM_HIP_UNSUPPORTED, "paged decode grid exceeds the launch limit");
       args.grid_y = p.kv_heads;
       const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
-      if (p.head_size == 96) {
-        if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
-          status = launch_stream_group<QE, false, 96>(args, grid, stream);
-        } else if (steps < 8) {
-          status = launch_stream<QE, false, 1, 1, 96>(args, grid, stream);
-        } else {
-          status = launch_stream<QE, false, 4, 1, 96>(args, grid, stream);
-        }
+      if (p.head_size == 80) {
+        status = launch_stream_rot<QE, 80>(args, grid, steps, stream);
+      } else if (p.head_size == 96) {
+        status = launch_stream_rot<QE, 96>(args, grid, steps, stream);
+      } else if (p.head_size == 112) {
+        status = launch_stream_rot<QE, 112>(args, grid, steps, stream);
       } else if (p.head_size == 256) {
         // 32 KiB of LDS per wave: two items per grouped workgroup, and the
         // 4-wave split (129 KiB, one workgroup per CU) only for grids under
