@@ -1188,15 +1188,22 @@ struct StreamDecoder {
   // stage holds rows at a 192-byte pitch; a row's chunks are rotated by
   // 3 (r >> 2) (mod 12), which puts the four rows that share a 256-byte bank
   // window at distinct chunk offsets.
-  // Head sizes 80 and 112 take the same layout: rows of 10 or 14 chunks, a
+  // Head sizes 80 and 112 take the same layout unrotated: rows of 10 or 14 chunks, a
   // tensor's step rounded up to whole DMA instructions (the spare lanes load
   // a valid chunk into the unused tail), QK over 3 or 4 operand chunks with
   // the chunks past the row read as zero.
   static constexpr bool kRot = kD == 80 || kD == 96 || kD == 112;
   static constexpr uint32_t kRowChunks = kD / 8;
   static constexpr int kRotDma = (kStep * kRowChunks + 63) / 64;  // DMA instructions per tensor per step
+  // Rotation of row r (in chunks); rot_slot places chunk `chunk` of row r.
+  // Rows of 160 and 224 bytes (head sizes 80, 112) measured free of bank
+  // conflicts unrotated (the 3 (r >> 2) rotation cost them 20 and 28 cycles
+  // per step).
+  static __device__ __forceinline__ uint32_t rot_shift(uint32_t r) {
+    return kD == 96 ? (3U * (r >> 2)) % kRowChunks : 0U;
+  }
   static __device__ __forceinline__ uint32_t rot_slot(uint32_t r, uint32_t chunk) {
-    return (chunk + 3U * (r >> 2)) % kRowChunks;
+    return (chunk + rot_shift(r)) % kRowChunks;
   }
   // Byte offset of 16-byte chunk ch of row t in the 16-bit V tile.
   static __device__ __forceinline__ uint32_t vt_off(uint32_t t, uint32_t ch) {
@@ -1275,7 +1282,7 @@ struct StreamDecoder {
         const uint32_t idx = 64U * i + lane;
         const bool spare = idx >= kStep * kRowChunks;  // past the step's rows: reload row 15, chunk 0
         const uint32_t r = spare ? kStep - 1 : idx / kRowChunks, slot = spare ? 0U : idx % kRowChunks;
-        const uint32_t logical = spare ? 0U : (slot + kRowChunks - (3U * (r >> 2)) % kRowChunks) % kRowChunks;
+        const uint32_t logical = spare ? 0U : (slot + kRowChunks - rot_shift(r)) % kRowChunks;
         w_voff[i] = static_cast<uint32_t>(r * kstride_p) + (logical << 4);
         w_voff[kRotDma + i] = static_cast<uint32_t>(r * vstride_p) + (logical << 4);
       }
