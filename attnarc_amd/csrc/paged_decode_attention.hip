@@ -8,9 +8,9 @@
 //
 // Kernels
 //   decode_stream_kernel / decode_stream_group_kernel
-//                        the main path: 16-bit query, D = Dv = 64, 128 or 256
-//                        (native or FP8 E4M3FN cache) or 80, 96, 112 (native),
-//                        up to 32 query heads per KV head (16 at 80-112 and 256),
+//                        the main path: 16-bit query, D = Dv = 64, 80, 96,
+//                        112, 128 or 256 (native or FP8 E4M3FN cache), up to
+//                        32 query heads per KV head (16 at 80-112 and 256),
 //                        power-of-two blocks >= 16. One wave per (sequence,
 //                        partition, KV head) item streams 16-token steps: K
 //                        and V rows go to LDS by DMA (swizzled), QK^T and PV
@@ -1176,9 +1176,8 @@ constexpr int kStreamStagesFp8 = 2;
 // of 256 bytes four per instruction).
 template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
-  static_assert(kD == kDim || kD == 64 || (kD == 256 && kHT == 1) ||
-                    ((kD == 80 || kD == 96 || kD == 112) && kHT == 1 && !kFp8),
-                "head size 64, 128, 256 with one head tile, or 80 / 96 / 112 with one head tile and a 16-bit cache");
+  static_assert(kD == kDim || kD == 64 || ((kD == 80 || kD == 96 || kD == 112 || kD == 256) && kHT == 1),
+                "head size 64, 128, or 80 / 96 / 112 / 256 with one head tile");
   static constexpr bool kNarrow = kD == 64 && !kFp8;         // 16-bit rows of 128 bytes
   static constexpr bool kF8Narrow = kD == 64 && kFp8;        // FP8 rows of 64 bytes
   static constexpr bool kWide = kD == 256 && !kFp8;          // 16-bit rows of 512 bytes
@@ -1191,9 +1190,14 @@ struct StreamDecoder {
   // tensor's step rounded up to whole DMA instructions (the spare lanes load
   // a valid chunk into the unused tail), QK over 3 or 4 operand chunks with
   // the chunks past the row read as zero.
+  // FP8 rows at these head sizes (80, 96 or 112 bytes) are kept unrotated
+  // and contiguous in LDS; the converted 16-bit V tile takes the rotated
+  // layout.
   static constexpr bool kRot = kD == 80 || kD == 96 || kD == 112;
-  static constexpr uint32_t kRowChunks = kD / 8;
-  static constexpr int kRotDma = (kStep * kRowChunks + 63) / 64;  // DMA instructions per tensor per step
+  static constexpr bool kF8Rot = kRot && kFp8;
+  static constexpr uint32_t kRowChunks = kD / 8;               // 16-byte chunks of a 16-bit row
+  static constexpr uint32_t kSrcChunks = kFp8 ? kD / 16 : kD / 8;  // 16-byte chunks of a cache row
+  static constexpr int kRotDma = (kStep * kSrcChunks + 63) / 64;  // DMA instructions per tensor per step
   // Rotation of row r (in chunks); rot_slot places chunk `chunk` of row r.
   // Head size 96: 2 (r >> 2). Rows r and r + 4 share bank offsets at the
   // 192-byte pitch, and the shift interleaves their 32-byte pieces in the
@@ -1214,7 +1218,9 @@ struct StreamDecoder {
   }
   static constexpr uint32_t kPitch = kD * 2;  // bytes between consecutive tokens' rows in a 16-bit tile
   static constexpr int kDt = kD / 16;         // 16-dim PV tiles
-  static constexpr int kKc = (kD + 31) / 32;  // 32-dim QK operand chunks (the last one zero-padded)
+  // 32-dim QK operand chunks (the last ones zero-padded); FP8 operands pair
+  // them over 64 dims.
+  static constexpr int kKc = kFp8 ? 2 * ((kD + 63) / 64) : (kD + 31) / 32;
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
@@ -1222,7 +1228,7 @@ struct StreamDecoder {
   // in place. FP8: kStages stages of [K bytes 2 KiB | V bytes 2 KiB], then
   // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
   static constexpr int kStages = kFp8 ? kStreamStagesFp8 : kStreamStages;
-  static constexpr uint32_t kF8TileBytes = kStep * kD;  // FP8 bytes of one tensor's step
+  static constexpr uint32_t kF8TileBytes = kRot ? kRotDma * 1024 : kStep * kD;  // FP8 bytes of one tensor's step
   static constexpr uint32_t kVOff = kRot ? kRotDma * 1024 : kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kVOff;
   static constexpr uint32_t kVTileOff = kStages * kStageBytes;  // FP8: converted V tile
@@ -1279,9 +1285,9 @@ struct StreamDecoder {
 #pragma unroll
       for (int i = 0; i < kRotDma; ++i) {
         const uint32_t idx = 64U * i + lane;
-        const bool spare = idx >= kStep * kRowChunks;  // past the step's rows: reload row 15, chunk 0
-        const uint32_t r = spare ? kStep - 1 : idx / kRowChunks, slot = spare ? 0U : idx % kRowChunks;
-        const uint32_t logical = spare ? 0U : (slot + kRowChunks - rot_shift(r)) % kRowChunks;
+        const bool spare = idx >= kStep * kSrcChunks;  // past the step's rows: reload row 15, chunk 0
+        const uint32_t r = spare ? kStep - 1 : idx / kSrcChunks, slot = spare ? 0U : idx % kSrcChunks;
+        const uint32_t logical = spare || kFp8 ? slot : (slot + kRowChunks - rot_shift(r)) % kRowChunks;
         w_voff[i] = static_cast<uint32_t>(r * kstride_p) + (logical << 4);
         w_voff[kRotDma + i] = static_cast<uint32_t>(r * vstride_p) + (logical << 4);
       }
@@ -1353,7 +1359,8 @@ struct StreamDecoder {
 #pragma unroll
       for (int i = 0; i < kRotDma; ++i) vm_load16_lds_sv(w_voff[i], kb, stage + i * 1024);
 #pragma unroll
-      for (int i = 0; i < kRotDma; ++i) vm_load16_lds_sv(w_voff[kRotDma + i], vb, stage + kVOff + i * 1024);
+      for (int i = 0; i < kRotDma; ++i)
+        vm_load16_lds_sv(w_voff[kRotDma + i], vb, stage + (kFp8 ? kF8TileBytes : kVOff) + i * 1024);
     } else if constexpr (kF8Narrow) {
       vm_load16_lds_sv(f8_k_voff[0], kb, stage);
       vm_load16_lds_sv(f8_v_voff[0], vb, stage + kF8TileBytes);
@@ -1393,7 +1400,13 @@ struct StreamDecoder {
   // dims); the half depends on g so that the two lane groups served together
   // read different banks.
   __device__ __forceinline__ vec8 k_operand(const uint8_t* stage, int kc) const {
-    if constexpr (kRot) {
+    if constexpr (kF8Rot) {
+      const uint32_t chunk = (static_cast<uint32_t>(kc) >> 1) * 4 + g;  // FP8 chunk of 16 dims
+      const uint2 w = *reinterpret_cast<const uint2*>(stage + c * kD + (chunk < kSrcChunks ? chunk : 0U) * 16 +
+                                                      ((kc ^ g) & 1U) * 8);
+      if (chunk >= kSrcChunks) return vec8{};  // dims past the head size
+      return Ops::from_fp8(w.x, w.y);
+    } else if constexpr (kRot) {
       const uint32_t chunk = static_cast<uint32_t>(kc) * 4 + g;
       const uint32_t slot = rot_slot(c, chunk < kRowChunks ? chunk : 0U);
       const vec8 k = *reinterpret_cast<const vec8*>(stage + c * kPitch + slot * 16);
@@ -1436,6 +1449,21 @@ struct StreamDecoder {
   // `up` lanes store the upper 16-bit chunk first) keep every read and every
   // store free of bank conflicts.
   __device__ __forceinline__ void stage_v_fp8(const uint8_t* stage, uint8_t* tile, uint32_t t0) const {
+    if constexpr (kF8Rot) {
+      // Rows of 5, 6 or 7 FP8 chunks: lanes take chunks by flat index.
+#pragma unroll
+      for (uint32_t it = 0; it < (kStep * kSrcChunks + 63) / 64; ++it) {
+        const uint32_t idx = it * 64U + lane;
+        if (idx < kStep * kSrcChunks) {
+          const uint32_t t = idx / kSrcChunks, lc = idx % kSrcChunks;
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(stage + kF8TileBytes + t * kD + lc * 16);
+          const u32x4 w = t0 + t < len ? raw : u32x4{0U, 0U, 0U, 0U};
+          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc)) = Ops::from_fp8(w[0], w[1]);
+          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc + 1)) = Ops::from_fp8(w[2], w[3]);
+        }
+      }
+      return;
+    }
     constexpr uint32_t kLaneChunks = kD / 64;  // 16-byte FP8 chunks per lane
     const uint32_t t = kF8Wide ? (lane & 15U) : (lane >> 2);
     const uint32_t q = kF8Wide ? (lane >> 4) : (lane & 3U);
@@ -1740,7 +1768,8 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
         const bool live = item.h0 + ht * 16U + dec.c < a.group;
 #pragma unroll
         for (int kc = 0; kc < Dec::kKc; ++kc) {
-          const bool in_row = kFp8 || kc * 32U + dec.g * 8U < kD;
+          const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
+          const bool in_row = dim < kD;
           dec.qb[ht][kc] = __builtin_bit_cast(vec8, live && in_row ? qw[ht][kc] : u32x4{0U, 0U, 0U, 0U});
         }
       }
@@ -2589,11 +2618,11 @@ int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
 
 // Head sizes 80, 96 and 112 (16-bit cache, one head tile): the launch shapes
 // of head size 128.
-template <typename QE, uint32_t kD>
+template <typename QE, bool kFp8, uint32_t kD>
 int launch_stream_rot(const DecodeArgs& args, uint64_t grid, uint32_t steps, hipStream_t stream) {
-  if (grid >= 4096 || (grid >= 1024 && steps >= 8)) return launch_stream_group<QE, false, kD>(args, grid, stream);
-  if (steps < 8) return launch_stream<QE, false, 1, 1, kD>(args, grid, stream);
-  return launch_stream<QE, false, 4, 1, kD>(args, grid, stream);
+  if (grid >= 4096 || (grid >= 1024 && steps >= 8)) return launch_stream_group<QE, kFp8, kD>(args, grid, stream);
+  if (steps < 8) return launch_stream<QE, kFp8, 1, 1, kD>(args, grid, stream);
+  return launch_stream<QE, kFp8, 4, 1, kD>(args, grid, stream);
 }
 
 // The streaming kernel needs steps that stay inside one block (power-of-two
@@ -2629,7 +2658,7 @@ bool wide_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uin
 // KV head.
 bool rot_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
                uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
-  return (dtype == kF16 || dtype == kBf16) && cache_encoding == LOOM_HIP_KV_CACHE_NATIVE &&
+  return (dtype == kF16 || dtype == kBf16) && cache_encoding <= LOOM_HIP_KV_CACHE_FP8_E4M3 &&
          (head_size == 80 || head_size == 96 || head_size == 112) && value_head_size == head_size &&
          query_heads / kv_heads <= 16 && is_pow2(block_size) && block_size >= kStep;
 }
@@ -2817,11 +2846,14 @@ int run_typed(const Problem& p, hipStream_t stream) {
       args.grid_y = p.kv_heads;
       const uint32_t steps = (partition_tokens + kStep - 1) / kStep;
       if (p.head_size == 80) {
-        status = launch_stream_rot<QE, 80>(args, grid, steps, stream);
+        status = fp8 ? launch_stream_rot<QE, true, 80>(args, grid, steps, stream)
+                     : launch_stream_rot<QE, false, 80>(args, grid, steps, stream);
       } else if (p.head_size == 96) {
-        status = launch_stream_rot<QE, 96>(args, grid, steps, stream);
+        status = fp8 ? launch_stream_rot<QE, true, 96>(args, grid, steps, stream)
+                     : launch_stream_rot<QE, false, 96>(args, grid, steps, stream);
       } else if (p.head_size == 112) {
-        status = launch_stream_rot<QE, 112>(args, grid, steps, stream);
+        status = fp8 ? launch_stream_rot<QE, true, 112>(args, grid, steps, stream)
+                     : launch_stream_rot<QE, false, 112>(args, grid, steps, stream);
       } else if (p.head_size == 256) {
         // 32 KiB of LDS per wave: two items per grouped workgroup, and the
         // 4-wave split (129 KiB, one workgroup per CU) only for grids under

@@ -192,13 +192,13 @@ def test_capability_query():
     s, reason, fam = ops.supports(2, 0, 4, 8, 8, 96, 96, 64, 16, 16, 256, 0.102)
     assert (s, fam) == (0, "mfma-stream")  # head size 96, 16-bit cache: 192-byte rows
     s, reason, fam = ops.supports(2, 1, 4, 8, 8, 96, 96, 64, 16, 16, 256, 0.102)
-    assert (s, fam) == (0, "vector")  # FP8 cache at head size 96: general kernel
+    assert (s, fam) == (0, "mfma-stream")  # FP8 cache at head size 96: 96-byte rows
     s, reason, fam = ops.supports(2, 0, 4, 8, 8, 80, 80, 64, 16, 16, 256, 0.11)
     assert (s, fam) == (0, "mfma-stream")  # head size 80, 16-bit cache: 160-byte rows
     s, reason, fam = ops.supports(2, 0, 4, 8, 8, 112, 112, 64, 16, 16, 256, 0.094)
     assert (s, fam) == (0, "mfma-stream")  # head size 112, 16-bit cache: 224-byte rows
     s, reason, fam = ops.supports(2, 1, 4, 8, 8, 80, 80, 64, 16, 16, 256, 0.11)
-    assert (s, fam) == (0, "vector")  # FP8 cache at head size 80: general kernel
+    assert (s, fam) == (0, "mfma-stream")  # FP8 cache at head size 80: 80-byte rows
     s, reason, fam = ops.supports(2, 0, 4, 8, 8, 72, 72, 64, 16, 16, 256, 0.11)
     assert (s, fam) == (0, "vector")  # head size 72: general kernel
     s, reason, fam = ops.supports(2, 0, 4, 16, 8, 256, 256, 64, 16, 16, 256, 0.0625)

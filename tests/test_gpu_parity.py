@@ -388,27 +388,31 @@ def test_stream_kernel_grouped_mid_grid(dtype, head_size, encoding, layout):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("layout", ["NHD", "HND"])
 @pytest.mark.parametrize("head", [80, 96, 112])
+@pytest.mark.parametrize("encoding", ["native", "fp8"])
 @pytest.mark.parametrize("shape,partition_tokens", [
     ((4, 32, 32, [700, 1, 33, 1500]), 512),     # MHA (Phi-2 / Phi-3 shapes), split over 4 waves
     ((3, 16, 4, [90, 17, 300]), 64),            # one wave per item, 32-token blocks below
     ((2, 16, 2, [400, 129]), 0),                # single partition, 8 heads per KV head
     ((64, 32, 32, [150 - (i % 23) for i in range(64)]), 64),  # >= 4096 items: grouped launch
 ])
-def test_stream_kernel_rotated_head_sizes(dtype, layout, head, shape, partition_tokens):
-    """Head sizes 80, 96 and 112 with a 16-bit cache on the streaming kernel
-    (rows of 10, 12 or 14 chunks at rotated slots; the QK operand chunks past
-    the head size are zero)."""
+def test_stream_kernel_rotated_head_sizes(dtype, layout, head, encoding, shape, partition_tokens):
+    """Head sizes 80, 96 and 112 on the streaming kernel: 16-bit caches (rows
+    of 10, 12 or 14 chunks, rotated at head size 96) or FP8 caches (rows of 5,
+    6 or 7 chunks, converted into the 16-bit V layout); the QK operand chunks
+    past the head size are zero."""
     B, Hq, Hkv, lengths = shape
     bs = 32 if partition_tokens == 64 and B == 3 else 16
     full = (B, Hq, Hkv, head, head, bs, lengths)
-    case = case_from(full, dtype, seed=83 + head, layout=layout, partition_tokens=partition_tokens)
-    _, _, fam = ops.supports(2, 0, B, Hq, Hkv, head, head, case.num_blocks, bs, case.max_blocks_per_sequence,
+    case = case_from(full, dtype, seed=83 + head, layout=layout, partition_tokens=partition_tokens,
+                     cache_encoding=encoding)
+    enc = 1 if encoding == "fp8" else 0
+    _, _, fam = ops.supports(2, enc, B, Hq, Hkv, head, head, case.num_blocks, bs, case.max_blocks_per_sequence,
                              case.max_sequence_length, case.scale)
     assert fam == "mfma-stream"
     out, lse = workloads.run_case(case, return_lse=True)
     torch.cuda.synchronize()
     expected, want_lse = oracle_expected(case)
-    assert_parity(out, expected, dtype, f"d{head} {full[:6]} part{partition_tokens} {layout}")
+    assert_parity(out, expected, dtype, f"d{head} {full[:6]} part{partition_tokens} {encoding} {layout}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
