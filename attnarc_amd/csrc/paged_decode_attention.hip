@@ -1203,8 +1203,12 @@ struct StreamDecoder {
   // 192-byte pitch, and the shift interleaves their 32-byte pieces in the
   // transposed reads (8 rows per pass); measured free of bank conflicts, where
   // 3 (r >> 2) cost 24 cycles per step. Rows of 160 and 224 bytes (head sizes
-  // 80, 112) measured conflict-free unrotated.
-  static __device__ __forceinline__ uint32_t rot_shift(uint32_t r) { return kD == 96 ? 2U * (r >> 2) : 0U; }
+  // 80, 112) measured conflict-free unrotated. The FP8 path's converted V
+  // tile stays unrotated: its conversion stores (8 lanes over 128 bytes of
+  // banks at a time) collide in the rotated layout.
+  static __device__ __forceinline__ uint32_t rot_shift(uint32_t r) {
+    return kD == 96 && !kFp8 ? 2U * (r >> 2) : 0U;
+  }
   static __device__ __forceinline__ uint32_t rot_slot(uint32_t r, uint32_t chunk) {
     return (chunk + rot_shift(r)) % kRowChunks;
   }
@@ -1458,8 +1462,12 @@ struct StreamDecoder {
           const uint32_t t = idx / kSrcChunks, lc = idx % kSrcChunks;
           const u32x4 raw = *reinterpret_cast<const u32x4*>(stage + kF8TileBytes + t * kD + lc * 16);
           const u32x4 w = t0 + t < len ? raw : u32x4{0U, 0U, 0U, 0U};
-          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc)) = Ops::from_fp8(w[0], w[1]);
-          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc + 1)) = Ops::from_fp8(w[2], w[3]);
+          const vec8 lo = Ops::from_fp8(w[0], w[1]), hi = Ops::from_fp8(w[2], w[3]);
+          // Lanes 4..7 of each eight store their upper chunk first, which
+          // spreads each store's eight lanes over distinct bank quarters.
+          const uint32_t up = (lane >> 2) & 1U;
+          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc + up)) = up ? hi : lo;
+          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc + 1 - up)) = up ? lo : hi;
         }
       }
       return;
