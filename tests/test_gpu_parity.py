@@ -289,6 +289,7 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("encoding", ["native", "fp8"])
 @pytest.mark.parametrize("layout", ["NHD", "HND"])
 @pytest.mark.parametrize("shape,partition_tokens", [
@@ -298,15 +299,15 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
     ((3, 71, 1, 64, 64, 16, [513, 17, 1600]), 512),        # group of 71 at head size 64: three waves, the last 7 heads live
     ((2, 80, 2, 64, 64, 16, [640, 90]), 64),               # group of 40, 64-token partitions
 ])
-def test_stream_kernel_wide_groups(encoding, layout, shape, partition_tokens):
+def test_stream_kernel_wide_groups(dtype, encoding, layout, shape, partition_tokens):
     """Groups of 33-128 query heads per KV head: one workgroup per item, each
     wave computing 32 heads of the group from the same K/V rows."""
     B, Hq, Hkv, D, Dv, bs, lengths = shape
-    dtype = torch.bfloat16
     case = case_from(shape, dtype, seed=81, layout=layout, partition_tokens=partition_tokens,
                      cache_encoding=encoding)
     enc = 1 if encoding == "fp8" else 0
-    _, _, fam = ops.supports(2, enc, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
+    qdt = 2 if dtype == torch.bfloat16 else 1
+    _, _, fam = ops.supports(qdt, enc, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
                              case.max_sequence_length, case.scale)
     assert fam == "mfma-stream"
     out, lse = workloads.run_case(case, return_lse=True)
