@@ -1566,7 +1566,6 @@ struct StreamDecoder {
 struct WorkItem {
   uint32_t seq, part, kvh, len;
   bool valid;
-  uint32_t h0;  // first query head of the group this wave computes (0 below 33 heads)
 };
 
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane) {
@@ -1756,7 +1755,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       u32x4 qw[kHT][Dec::kKc];
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) {
-        const uint32_t h = min(item.h0 + ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
+        const uint32_t h = min(ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
         const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
                                (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kD;
 #pragma unroll
@@ -1773,7 +1772,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       }
 #pragma unroll
       for (int ht = 0; ht < kHT; ++ht) {
-        const bool live = item.h0 + ht * 16U + dec.c < a.group;
+        const bool live = ht * 16U + dec.c < a.group;
 #pragma unroll
         for (int kc = 0; kc < Dec::kKc; ++kc) {
           const uint32_t dim = kFp8 ? ((kc >> 1) * 64 + dec.g * 16 + ((kc ^ dec.g) & 1U) * 8) : (kc * 32 + dec.g * 8);
@@ -1821,8 +1820,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   if (kSplit == 1) {
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
-      if (item.h0 + ht * 16U + dec.c < a.group)
-        store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + item.h0 + ht * 16U, part, v_scale, lt[ht]);
+      if (ht * 16U + dec.c < a.group) store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
     }
     return;
   }
