@@ -445,7 +445,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the decode shards by sequence/KV head with no exchange; see DESIGN.md). "
+              "(the decode shards by sequence or KV head with no exchange between GPUs). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 
