@@ -1446,8 +1446,8 @@ struct StreamDecoder {
 
   // FP8 V bytes of a stage -> the wave's swizzled 16-bit V tile (rows past
   // the sequence end become zero). Head sizes 64 and 128: lane handles kD / 4
-  // bytes of token lane >> 2; head size 256: lane handles 64 bytes of token
-  // lane & 15. 16-byte LDS reads are served 16 lanes at a time over 256 bytes
+  // bytes of token lane >> 2; head size 256: lane handles four 16-byte chunks
+  // of token lane & 15. 16-byte LDS reads are served 16 lanes at a time over 256 bytes
   // of banks, 16-byte writes 8 lanes at a time over 128 bytes; the row
   // mapping, the V swizzle and the order of each lane's two stores (the
   // `up` lanes store the upper 16-bit chunk first) keep every read and every
@@ -1481,7 +1481,10 @@ struct StreamDecoder {
     const uint32_t swz = kF8Wide ? (t & 15U) : kF8Narrow ? ((t >> 2) & 3U) : ((t >> 1) & 7U);
 #pragma unroll
     for (uint32_t h = 0; h < kLaneChunks; ++h) {
-      const uint32_t lc = q * kLaneChunks + h;  // logical 16-byte chunk of the FP8 row
+      // Logical 16-byte chunk of the FP8 row: head size 256 interleaves the
+      // four lane groups (q, q + 4, q + 8, q + 12), which measured free of
+      // read conflicts where q * 4 + h read 16 conflict cycles per step.
+      const uint32_t lc = kF8Wide ? q + 4U * h : q * kLaneChunks + h;
       const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ swz) << 4));
       const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
       // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each).
