@@ -217,6 +217,24 @@ def test_capability_query():
     assert (s, fam) == (0, "vector")  # groups above 128 heads: general kernel
     s, reason, fam = ops.supports(2, 0, 8, 64, 1, 128, 128, 8192, 8, 512, 4096, 0.088)
     assert (s, fam) == (0, "vector")  # wide groups need blocks of at least 16 tokens
+
+
+def test_capability_query_family_boundaries():
+    """The streaming families at the edges of each launch shape."""
+    def fam(dtype, enc, hq, hkv, d, bs=16):
+        s, _, f = ops.supports(dtype, enc, 8, hq, hkv, d, d, 8192, bs, 512 * 16 // bs, 4096, d ** -0.5)
+        assert s == 0
+        return f
+    assert fam(2, 0, 32, 1, 128) == "mfma-stream"   # 32 heads: two tiles in one wave
+    assert fam(2, 0, 33, 1, 128) == "mfma-stream"   # 33 heads: the wide-group kernel, 2 waves
+    assert fam(1, 1, 128, 1, 128) == "mfma-stream"  # 128 heads, F16, FP8 cache: 4 waves
+    assert fam(2, 1, 129, 1, 128) == "vector"       # above 128 heads
+    assert fam(2, 0, 96, 1, 64) == "mfma-stream"    # 96 heads at head size 64: 3 waves
+    assert fam(2, 0, 64, 1, 96) == "vector"         # wide groups only at head sizes 64 and 128
+    assert fam(2, 1, 16, 1, 112) == "mfma-stream"   # FP8 at head size 112
+    assert fam(2, 1, 17, 1, 112) == "vector"        # head sizes 80-112 take one head tile
+    assert fam(0, 0, 8, 8, 128) == "vector"         # F32 queries: general kernel
+    assert fam(2, 0, 16, 1, 80, bs=8) == "vector"   # streaming steps need blocks of 16 or more
     s, reason, fam = ops.supports(2, 0, 8, 32, 1, 128, 128, 65536, 16, 8192, 131072, 0.088)
     assert (s, fam) == (0, "mfma-stream")
     s, reason, _ = ops.supports(7, 0, 4, 8, 8, 64, 64, 64, 16, 16, 256, 0.125)
