@@ -29,6 +29,9 @@ F32, F16, BF16 = 0, 1, 2
 ROPE_PAGED_KV_WRITE = 5
 PAGED_DECODE_ATTENTION = 9
 KERNEL_DECODE, KERNEL_MERGE, KERNEL_ROPE = 0, 1, 2
+# F32 elements of the per-device array behind the no-allocation entry point
+# (LOOM_HIP_STATIC_WORKSPACE_ELEMENTS in include/loom_hip.h).
+STATIC_WORKSPACE_ELEMENTS = 16 * 1024 * 1024
 
 # Bridge status codes (include/loom_hip_bridge.h); they differ from the
 # unchecked library's codes above, as loom_cuda_bridge.h's do from loom_cuda.h's.
@@ -43,6 +46,7 @@ F = ctypes.c_float
 _BASE = [P, P, P, P, P, P] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _SPLIT = [P, P, P, P, P, P, P, U64] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _EXT = [P, P, P, P, P, P, P, P, P, P, U64] + [U32] * 9 + [U64] * 6 + [U32, U32, U32, F, P]
+_NO_ALLOC = [U32] + [P] * 9 + [U32] * 9 + [U64] * 6 + [U32, U32, U32, F, P]
 _ROPE = [P] * 10 + [U32] * 12 + [U64] * 12 + [U32, P]
 # Checked bridge (include/loom_hip_bridge.h).
 _BRIDGE_ROPE = [U32, U32] + [P, U64] * 10 + [U32] * 10 + [U64] * 12 + [U32, P]
@@ -60,6 +64,7 @@ SIGNATURES = {
     "loom_hip_paged_decode_attention_extended_f32": (_EXT, ctypes.c_int),
     "loom_hip_paged_decode_attention_extended_f16": (_EXT, ctypes.c_int),
     "loom_hip_paged_decode_attention_extended_bf16": (_EXT, ctypes.c_int),
+    "loom_hip_paged_decode_attention_extended_no_alloc": (_NO_ALLOC, ctypes.c_int),
     "loom_hip_paged_decode_attention_supports": (
         [U32] * 11 + [F, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p)],
         ctypes.c_int,

@@ -2418,6 +2418,7 @@ struct Problem {
   uint32_t max_blocks_per_sequence, max_sequence_length;
   uint32_t partition_tokens;  // 0 = one partition per sequence
   float scale;
+  bool static_workspace;  // split-K states go to the library's per-device array
 };
 
 size_t elem_size(uint32_t dtype) { return dtype == kF32 ? 4 : 2; }
@@ -2516,7 +2517,11 @@ int validate(const Problem& p) {
   if (parts > 1) {
     need = static_cast<uint64_t>(p.sequences) * p.query_heads * parts * (p.value_head_size + 2ULL);
   }
-  if (need == 0) {
+  if (p.static_workspace) {
+    if (need > LOOM_HIP_STATIC_WORKSPACE_ELEMENTS)
+      return fail(LOOM_HIP_UNSUPPORTED,
+                  "split-K states exceed the static workspace (LOOM_HIP_STATIC_WORKSPACE_ELEMENTS F32 elements)");
+  } else if (need == 0) {
     if (p.workspace != nullptr || p.workspace_elements != 0)
       return fail(LOOM_HIP_INVALID_ARGUMENT,
                   "this shape uses a single partition; the workspace must be null with zero elements");
@@ -2965,11 +2970,50 @@ int device_available() {
   return LOOM_HIP_SUCCESS;
 }
 
-int run(const Problem& p, void* stream) {
+// Split-K scratch of the no-allocation entry point: one array per device,
+// resident from module load until the process ends. Host code never uses the
+// array's name as an address: the per-device address comes from
+// hipGetSymbolAddress, called once per device with that device current.
+__device__ __align__(256) float scratch[LOOM_HIP_STATIC_WORKSPACE_ELEMENTS];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_address(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(LOOM_HIP_UNAVAILABLE, "no current HIP device");
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(LOOM_HIP_UNSUPPORTED, "device ordinal beyond the static workspace table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      return fail(LOOM_HIP_LAUNCH_ERROR, "hipGetSymbolAddress of the static workspace failed");
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return LOOM_HIP_SUCCESS;
+}
+
+int run(Problem p, void* stream) {
   int status = validate(p);
   if (status != LOOM_HIP_SUCCESS) return status;
   status = device_available();
   if (status != LOOM_HIP_SUCCESS) return status;
+  if (p.static_workspace) {
+    const uint64_t parts = parts_for(p.max_sequence_length, p.partition_tokens);
+    if (parts > 1) {
+      status = scratch_address(&p.workspace);
+      if (status != LOOM_HIP_SUCCESS) return status;
+      p.workspace_elements = LOOM_HIP_STATIC_WORKSPACE_ELEMENTS;
+    }
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (p.dtype) {
     case kF32: status = run_typed<F32Elem>(p, s); break;
@@ -3446,6 +3490,27 @@ int loom_hip_paged_decode_attention_extended_bf16(
                               max_blocks_per_sequence, max_sequence_length, partition_tokens,
                               scale),
              stream);
+}
+
+int loom_hip_paged_decode_attention_extended_no_alloc(
+    uint32_t dtype, const void* query, const void* key_cache, const void* value_cache,
+    const float* key_scales, const float* value_scales, const int32_t* block_tables,
+    const int32_t* sequence_lengths, void* output, float* lse, uint32_t sequences,
+    uint32_t query_heads, uint32_t kv_heads, uint32_t head_size, uint32_t value_head_size,
+    uint32_t num_blocks, uint32_t block_size, uint32_t cache_encoding, uint32_t scale_stride,
+    uint64_t key_block_stride, uint64_t key_page_stride, uint64_t key_head_stride,
+    uint64_t value_block_stride, uint64_t value_page_stride, uint64_t value_head_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length, uint32_t partition_tokens,
+    float scale, void* stream) {
+  Problem p = extended_problem(dtype, query, key_cache, value_cache, key_scales, value_scales,
+                               block_tables, sequence_lengths, output, lse, nullptr, 0, sequences,
+                               query_heads, kv_heads, head_size, value_head_size, num_blocks,
+                               block_size, cache_encoding, scale_stride, key_block_stride,
+                               key_page_stride, key_head_stride, value_block_stride,
+                               value_page_stride, value_head_stride, max_blocks_per_sequence,
+                               max_sequence_length, partition_tokens, scale);
+  p.static_workspace = true;
+  return run(p, stream);
 }
 
 }  // extern "C"

@@ -359,6 +359,7 @@ def paged_decode_attention_extended(
     lse: torch.Tensor | None = None,
     return_lse: bool = False,
     workspace: torch.Tensor | None = None,
+    no_alloc: bool = False,
 ):
     """Paged decode over native or FP8 E4M3 caches in NHD or HND layout.
 
@@ -367,7 +368,10 @@ def paged_decode_attention_extended(
     logical value is ``fp8_to_f32(byte) * scale[kv_head]``. With
     ``partition_tokens > 0`` each sequence is split into partitions of that
     many tokens merged by log-sum-exp; the F32 workspace is allocated here
-    unless given. Returns ``output`` or ``(output, lse)``.
+    unless given. ``no_alloc=True`` calls the no-allocation entry point
+    instead: the partial states go to the library's static per-device array
+    (``output`` and ``lse`` must then be given when they are wanted, and no
+    ``workspace`` is taken). Returns ``output`` or ``(output, lse)``.
     """
     _require_inference_tensors(query, key_cache, value_cache)
     if query.dim() != 3 or not query.is_contiguous():
@@ -413,6 +417,20 @@ def paged_decode_attention_extended(
         output = torch.empty((sequences, query_heads, dv), device=query.device, dtype=query.dtype)
     if lse is None and return_lse:
         lse = torch.empty((sequences, query_heads), device=query.device, dtype=torch.float32)
+    code = _DTYPE_CODES[query.dtype]
+    if no_alloc:
+        if workspace is not None:
+            raise RuntimeError("Loom paged decode no-allocation calls take no workspace")
+        with torch.cuda.device(query.device):
+            status = _native.lib().loom_hip_paged_decode_attention_extended_no_alloc(
+                code, _ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(key_scales), _ptr(value_scales),
+                _ptr(block_tables), _ptr(sequence_lengths), _ptr(output), _ptr(lse),
+                sequences, query_heads, hkv, head_size, dv, nb, bs, encoding, scale_stride,
+                *kstr, *vstr, int(block_tables.shape[1]), max_sequence_length, int(partition_tokens),
+                float(scale), _stream_handle(query.device),
+            )
+        _native.check(status, "Loom paged decode attention (no allocation)")
+        return (output, lse) if return_lse else output
     need = extended_workspace_elements(sequences, query_heads, dv, max_sequence_length, partition_tokens)
     if need and workspace is None:
         workspace = torch.empty(need, device=query.device, dtype=torch.float32)

@@ -231,6 +231,37 @@ int loom_hip_paged_decode_attention_extended_bf16(
     void* stream);
 
 /*
+ * No-allocation variant of loom_hip_paged_decode_attention_extended_*. It has
+ * no counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). `dtype` is a LoomHipDType; every other argument means
+ * what it means for the extended entry point of that dtype, and the results
+ * are the same. The split-K partial states go to a static array of
+ * LOOM_HIP_STATIC_WORKSPACE_ELEMENTS F32 elements (64 MiB) that the library
+ * holds on each device it runs on until the process ends. A call whose
+ * states need more (the extended sizing function's count) returns
+ * LOOM_HIP_UNSUPPORTED before launching anything. Nothing is allocated,
+ * freed or cleared by the call. All calls on one device share that device's
+ * array: calls that may overlap in time on one device (different streams,
+ * or different threads without ordering) race and must not be issued.
+ */
+#define LOOM_HIP_STATIC_WORKSPACE_ELEMENTS (16ULL * 1024ULL * 1024ULL)
+
+int loom_hip_paged_decode_attention_extended_no_alloc(
+    uint32_t dtype, const void* query, const void* key_cache,
+    const void* value_cache, const float* key_scales,
+    const float* value_scales, const int32_t* block_tables,
+    const int32_t* sequence_lengths, void* output, float* lse,
+    uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+    uint32_t head_size, uint32_t value_head_size, uint32_t num_blocks,
+    uint32_t block_size, uint32_t cache_encoding, uint32_t scale_stride,
+    uint64_t key_block_stride, uint64_t key_page_stride,
+    uint64_t key_head_stride, uint64_t value_block_stride,
+    uint64_t value_page_stride, uint64_t value_head_stride,
+    uint32_t max_blocks_per_sequence, uint32_t max_sequence_length,
+    uint32_t partition_tokens, float scale, void* stream);
+
+/*
  * Capability query. Replaces the PagedDecodeAttention arms of
  * CudaBackend::supports (crates/loom-cuda/src/cuda_backend.rs:112-134,
  * attention_dispatch.rs:330-344). Reports without launching work. Returns

@@ -276,3 +276,35 @@ def test_python_contract_errors_on_cpu_tensors():
     with pytest.raises(ValueError, match="inference-only"):
         ops.paged_decode_attention(query.requires_grad_(), cache, cache, torch.zeros((1, 1), dtype=torch.int32),
                                    torch.ones(1, dtype=torch.int32), max_sequence_length=8)
+
+
+def call_no_alloc(dtype=_native.BF16, **kw):
+    a = ext_args(**kw)
+    return _native.lib().loom_hip_paged_decode_attention_extended_no_alloc(
+        dtype, a["q"], a["k"], a["v"], a["ks"], a["vs"], a["tables"], a["lens"], a["out"], a["lse"],
+        a["B"], a["Hq"], a["Hkv"], a["D"], a["Dv"], a["NB"], a["bs"], a["enc"], a["sstride"],
+        a["kb"], a["kp"], a["kh"], a["vb"], a["vp"], a["vh"], a["maxb"], a["maxlen"], a["part"], a["scale"], None)
+
+
+def test_no_alloc_rejects_states_beyond_the_static_workspace():
+    # 128 x 64 heads x 256 partitions x 130 > 16 Mi elements: rejected on the host, before any device use.
+    need = 128 * 64 * 256 * 130
+    assert need > _native.STATIC_WORKSPACE_ELEMENTS
+    status = call_no_alloc(B=128, Hq=64, Hkv=8, NB=1 << 20, maxb=8192, maxlen=131072, part=512)
+    assert status == _native.UNSUPPORTED
+    assert "static workspace" in _native.last_error()
+
+
+@pytest.mark.parametrize("change", [dict(q=None), dict(out=None), dict(Hq=6, Hkv=4), dict(scale=0.0), dict(maxlen=257)])
+def test_no_alloc_validates_like_the_extended_entry_point(change):
+    assert call_no_alloc(**change) == _native.INVALID_ARGUMENT
+
+
+def test_no_alloc_rejects_unknown_dtype():
+    assert call_no_alloc(dtype=7) == _native.INVALID_ARGUMENT
+    assert "dtype" in _native.last_error()
+
+
+@no_device
+def test_no_alloc_valid_call_needs_a_device():
+    assert call_no_alloc(maxlen=256, part=64) == _native.UNAVAILABLE
