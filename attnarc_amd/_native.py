@@ -42,7 +42,8 @@ U32 = ctypes.c_uint32
 U64 = ctypes.c_uint64
 F = ctypes.c_float
 
-# (name, argtypes, restype) for every symbol declared in include/loom_hip.h.
+# (name, argtypes, restype) for every symbol declared in include/loom_hip.h,
+# include/loom_hip_bridge.h and include/loom_hip_views.h.
 _BASE = [P, P, P, P, P, P] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _SPLIT = [P, P, P, P, P, P, P, U64] + [U32] * 7 + [U64, U64, U32, U32, F, P]
 _EXT = [P, P, P, P, P, P, P, P, P, P, U64] + [U32] * 9 + [U64] * 6 + [U32, U32, U32, F, P]
@@ -51,6 +52,26 @@ _ROPE = [P] * 10 + [U32] * 12 + [U64] * 12 + [U32, P]
 # Checked bridge (include/loom_hip_bridge.h).
 _BRIDGE_ROPE = [U32, U32] + [P, U64] * 10 + [U32] * 10 + [U64] * 12 + [U32, P]
 _BRIDGE_DECODE = [U32] + [P, U64] * 7 + [U32] * 7 + [U64, U64, U32, U32, F, P]
+
+class TensorView(ctypes.Structure):
+    """``loom_hip_tensor_view`` (include/loom_hip_views.h)."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("device_index", ctypes.c_int32),
+        ("dtype", ctypes.c_uint32),
+        ("rank", ctypes.c_uint32),
+        ("sizes", ctypes.c_int64 * 5),
+        ("strides", ctypes.c_int64 * 5),
+    ]
+
+
+VIEW_F32, VIEW_F16, VIEW_BF16, VIEW_U8, VIEW_FP8_E4M3FN, VIEW_I32, VIEW_I64, VIEW_OTHER = 0, 1, 2, 3, 4, 5, 6, 255
+VIEWS_OK, VIEWS_CONTRACT, VIEWS_BRIDGE = 0, 1, 2
+_VIEWS = ctypes.POINTER(TensorView)
+D = ctypes.c_double
+I64 = ctypes.c_int64
+
 SIGNATURES = {
     "loom_hip_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "loom_hip_paged_decode_attention_f32": (_BASE, ctypes.c_int),
@@ -80,6 +101,12 @@ SIGNATURES = {
     "loom_hip_bridge_rope_paged_kv_write": (_BRIDGE_ROPE, ctypes.c_int),
     "loom_hip_bridge_paged_decode_workspace_elements": ([U32] * 10 + [F, ctypes.POINTER(U64)], ctypes.c_int),
     "loom_hip_bridge_paged_decode_attention": (_BRIDGE_DECODE, ctypes.c_int),
+    "loom_hip_views_last_error_message": ([], ctypes.c_char_p),
+    "loom_hip_views_paged_decode_check": ([_VIEWS, U32, I64, D], ctypes.c_int),
+    "loom_hip_views_paged_decode_workspace_elements": ([_VIEWS, I64, D, ctypes.POINTER(U64)], ctypes.c_int),
+    "loom_hip_views_paged_decode_attention": ([_VIEWS, I64, D, P, U64, P], ctypes.c_int),
+    "loom_hip_views_rope_paged_kv_check": ([_VIEWS], ctypes.c_int),
+    "loom_hip_views_rope_paged_kv_write": ([_VIEWS, U32, P], ctypes.c_int),
     "loom_hip_abi_version": ([], U32),
     "loom_hip_last_error_message": ([], ctypes.c_char_p),
     "loom_hip_launch_count": ([U32, ctypes.POINTER(U64)], ctypes.c_int),

@@ -16,6 +16,7 @@ SOURCES = [
     os.path.join(PKG_DIR, "csrc", "paged_decode_attention.hip"),
     os.path.join(PKG_DIR, "csrc", "rope_paged_kv.hip"),
     os.path.join(PKG_DIR, "csrc", "loom_hip_bridge.cpp"),
+    os.path.join(PKG_DIR, "csrc", "loom_hip_views.cpp"),
 ]
 LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip.so")
 PROBE_SOURCE = os.path.join(PKG_DIR, "csrc", "hbm_probe.hip")
@@ -34,13 +35,34 @@ HIPCC_FLAGS = [
 ]
 
 
-def _compile(sources, out: str, verbose: bool) -> None:
-    os.makedirs(os.path.dirname(out), exist_ok=True)
-    tmp = out + ".tmp"
-    cmd = [HIPCC, *HIPCC_FLAGS, *sources, "-o", tmp]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
+
+
+def _compile(sources, out: str, verbose: bool, incremental: bool = False) -> None:
+    """Compile each source to an object under _build/obj, then link ``out``.
+
+    With ``incremental`` an object newer than its source and every header is
+    reused (a developer convenience); ``build()`` recompiles everything.
+    """
+    obj_dir = os.path.join(os.path.dirname(out), "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    headers = [os.path.join(REPO_DIR, "include", h) for h in os.listdir(os.path.join(REPO_DIR, "include"))]
+    headers += [os.path.join(PKG_DIR, "csrc", h) for h in os.listdir(os.path.join(PKG_DIR, "csrc")) if h.endswith(".h")]
+    newest_header = max(os.path.getmtime(h) for h in headers)
+    objects = []
+    for src in sources:
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+        objects.append(obj)
+        if incremental and os.path.exists(obj) and os.path.getmtime(obj) > max(os.path.getmtime(src), newest_header):
+            continue
+        flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+        _run([HIPCC, *flags, "-c", src, "-o", obj + ".tmp"], verbose)
+        os.replace(obj + ".tmp", obj)
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIPCC_FLAGS, *objects, "-o", tmp], verbose)
     os.replace(tmp, out)
 
 
@@ -74,13 +96,15 @@ def _compile_adapter(verbose: bool) -> None:
     os.replace(tmp, ADAPTER_LIB_PATH)
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, incremental: bool = False) -> str:
     """Compile the kernel library, the HBM probe library and the torch adapter; returns the first's path."""
-    _compile(SOURCES, LIB_PATH, verbose)
-    _compile([PROBE_SOURCE], PROBE_LIB_PATH, verbose)
+    _compile(SOURCES, LIB_PATH, verbose, incremental)
+    _compile([PROBE_SOURCE], PROBE_LIB_PATH, verbose, incremental)
     _compile_adapter(verbose)
     return LIB_PATH
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    import sys
+
+    print(build(verbose=True, incremental="--incremental" in sys.argv))

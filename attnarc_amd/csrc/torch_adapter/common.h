@@ -1,13 +1,14 @@
-// Shared helpers of the loom-hip PyTorch Stable-ABI adapter.
+// Framework glue of the loom-hip PyTorch Stable-ABI adapter.
 //
-// The adapter is the MI355X counterpart of the reference's
-// python/csrc/{common.h, attention.cpp, rope_kv.cpp, telemetry.cpp,
-// torch_ops.cpp}: the same `loom_kernels` operator schema, the same tensor
-// contract checks and messages, the current HIP stream taken from torch, and
-// split-K workspaces allocated from the torch caching allocator (so calls are
-// graph-capturable). All launches go through the checked bridge of
-// include/loom_hip_bridge.h. Only the Stable ABI is used, so one build loads
-// into any torch release from the target version on.
+// The adapter does not check tensors itself. It describes every operand as a
+// loom_hip_tensor_view and hands the set to the library's view front end
+// (include/loom_hip_views.h), which holds each operator's tensor contract as
+// a table and submits through the checked bridge. What stays here is what
+// only torch can provide: the device guard, torch's current HIP stream, the
+// split-K workspace from the caching allocator (so a call under
+// torch.cuda.graph allocates from the graph's pool), and turning a refusal
+// into a torch error. Only the Stable ABI is used, so one build loads into
+// any torch release from the target version on.
 #pragma once
 
 #define TORCH_TARGET_VERSION (((0ULL + 2) << 56) | ((0ULL + 10) << 48))
@@ -20,90 +21,58 @@
 #include <torch/headeronly/core/ScalarType.h>
 #include <torch/headeronly/macros/Macros.h>
 
-#include <cmath>
 #include <cstdint>
-#include <initializer_list>
-#include <limits>
 
 #include "loom_hip_bridge.h"
+#include "loom_hip_views.h"
 
 namespace loom_hip::torch_adapter {
 
 using Tensor = torch::stable::Tensor;
 using ScalarType = torch::headeronly::ScalarType;
 
-// Makes the tensor's device current for the scope of a launch.
-class DeviceScope final {
- public:
-  explicit DeviceScope(const torch::stable::Device& device) : guard_(device.index()) {}
+inline uint32_t view_dtype(ScalarType t) {
+  switch (t) {
+    case ScalarType::Float: return LOOM_HIP_VIEW_F32;
+    case ScalarType::Half: return LOOM_HIP_VIEW_F16;
+    case ScalarType::BFloat16: return LOOM_HIP_VIEW_BF16;
+    case ScalarType::Byte: return LOOM_HIP_VIEW_U8;
+    case ScalarType::Float8_e4m3fn: return LOOM_HIP_VIEW_FP8_E4M3FN;
+    case ScalarType::Int: return LOOM_HIP_VIEW_I32;
+    case ScalarType::Long: return LOOM_HIP_VIEW_I64;
+    default: return LOOM_HIP_VIEW_OTHER;
+  }
+}
 
- private:
-  torch::stable::accelerator::DeviceGuard guard_;
-};
+// The view of a tensor as the library's contract tables see it. Ranks above
+// the view limit are passed as such and fail the contract's rank rule.
+inline loom_hip_tensor_view view_of(const Tensor& t) {
+  loom_hip_tensor_view v{};
+  v.data = t.const_data_ptr();
+  v.device_index = t.is_cuda() ? static_cast<int32_t>(t.device().index()) : -1;
+  v.dtype = view_dtype(t.scalar_type());
+  v.rank = static_cast<uint32_t>(t.dim());
+  for (int64_t d = 0; d < t.dim() && d < LOOM_HIP_VIEW_MAX_RANK; ++d) {
+    v.sizes[d] = t.size(d);
+    v.strides[d] = t.stride(d);
+  }
+  return v;
+}
 
-// torch's current stream on a device (a hipStream_t on ROCm builds).
+// Raises the library's refusal as a torch error: the contract's own message,
+// or the bridge's with the operation named.
+inline void raise_unless_ok(int status, const char* operation) {
+  if (status == LOOM_HIP_VIEWS_OK) return;
+  const char* message = loom_hip_views_last_error_message();
+  STD_TORCH_CHECK(status != LOOM_HIP_VIEWS_CONTRACT, message);
+  STD_TORCH_CHECK(false, "Loom HIP ", operation, " bridge failed: ", message);
+}
+
+// torch's current stream on the guarded device (a hipStream_t on ROCm).
 inline void* current_stream(int32_t device_index) {
   void* stream = nullptr;
   TORCH_ERROR_CODE_CHECK(aoti_torch_get_current_cuda_stream(device_index, &stream));
   return stream;
-}
-
-inline uint64_t tensor_nbytes(const Tensor& t) {
-  STD_TORCH_CHECK(t.numel() >= 0, "negative tensor element count");
-  const auto n = static_cast<uint64_t>(t.numel());
-  const auto e = static_cast<uint64_t>(t.element_size());
-  STD_TORCH_CHECK(e == 0 || n <= std::numeric_limits<uint64_t>::max() / e, "tensor byte size exceeds uint64");
-  return n * e;
-}
-
-inline uint32_t bridge_dtype(const Tensor& t) {
-  switch (t.scalar_type()) {
-    case ScalarType::Float: return LOOM_HIP_BRIDGE_F32;
-    case ScalarType::Half: return LOOM_HIP_BRIDGE_F16;
-    case ScalarType::BFloat16: return LOOM_HIP_BRIDGE_BF16;
-    default: break;
-  }
-  STD_TORCH_CHECK(false, "unsupported Loom bridge dtype");
-  return 0;
-}
-
-// Elements from the first to one past the last addressed element:
-// 1 + sum (size - 1) * stride over positive sizes and strides.
-inline uint64_t storage_span_elements(const Tensor& t) {
-  STD_TORCH_CHECK(t.numel() > 0, "Loom bridge tensors must contain at least one element");
-  uint64_t span = 1;
-  for (int64_t d = 0; d < t.dim(); ++d) {
-    STD_TORCH_CHECK(t.size(d) > 0 && t.stride(d) > 0, "Loom bridge requires positive tensor sizes and strides");
-    const auto extent = static_cast<uint64_t>(t.size(d) - 1);
-    const auto stride = static_cast<uint64_t>(t.stride(d));
-    STD_TORCH_CHECK(extent == 0 || stride <= (std::numeric_limits<uint64_t>::max() - span) / extent,
-                    "Loom tensor storage span exceeds the bridge ABI");
-    span += extent * stride;
-  }
-  return span;
-}
-
-inline void check_bridge_status(int status, const char* operation) {
-  STD_TORCH_CHECK(status == LOOM_HIP_BRIDGE_SUCCESS, "Loom HIP ", operation,
-                  " bridge failed: ", loom_hip_bridge_last_error_message(), " (status ", status, ")");
-}
-
-// Overlap of the byte ranges [data, data + numel * element_size).
-inline bool byte_ranges_overlap(const Tensor& a, const Tensor& b) {
-  const auto a0 = reinterpret_cast<uintptr_t>(a.const_data_ptr());
-  const auto b0 = reinterpret_cast<uintptr_t>(b.const_data_ptr());
-  const auto an = tensor_nbytes(a), bn = tensor_nbytes(b);
-  STD_TORCH_CHECK(an <= std::numeric_limits<uintptr_t>::max() - a0 && bn <= std::numeric_limits<uintptr_t>::max() - b0,
-                  "tensor byte range exceeds uintptr_t");
-  return a0 < b0 + bn && b0 < a0 + an;
-}
-
-// [blocks, block_size, heads, dim] with only the block stride allowed gaps.
-inline bool has_dense_nhd_inner_strides(const Tensor& t) {
-  if (t.dim() != 4) return false;
-  const int64_t block = t.size(1) * t.size(2) * t.size(3);
-  return t.stride(3) == 1 && t.stride(2) == t.size(3) && t.stride(1) == t.size(2) * t.size(3) &&
-         t.stride(0) >= block;
 }
 
 }  // namespace loom_hip::torch_adapter

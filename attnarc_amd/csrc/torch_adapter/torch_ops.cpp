@@ -1,6 +1,8 @@
 // Schema of the `loom_kernels` operators this library implements (the
 // paged-decode and RoPE+KV subset of python/csrc/torch_ops.cpp, identical
 // signatures) and the bridge telemetry ops (python/csrc/telemetry.cpp).
+#include <limits>
+
 #include "common.h"
 
 STABLE_TORCH_LIBRARY(loom_kernels, library) {
@@ -17,6 +19,15 @@ STABLE_TORCH_LIBRARY(loom_kernels, library) {
 }
 
 namespace loom_hip::torch_adapter {
+
+namespace {
+
+void check_bridge_status(int status, const char* operation) {
+  STD_TORCH_CHECK(status == LOOM_HIP_BRIDGE_SUCCESS, "Loom HIP ", operation,
+                  " bridge failed: ", loom_hip_bridge_last_error_message(), " (status ", status, ")");
+}
+
+}  // namespace
 
 int64_t bridge_abi_version() { return static_cast<int64_t>(loom_hip_bridge_abi_version()); }
 

@@ -1,9 +1,12 @@
 """PyTorch-facing paged decode attention over the loom-hip C ABI.
 
 Mirrors the reference's public Python surface
-(python/src/loom_kernels/ops/attention.py:1-154) and its Stable-ABI adapter
-(python/csrc/attention.cpp:5-162): same function names, argument meaning,
-default scale ``head_size ** -0.5`` and RuntimeError/ValueError behaviour.
+(python/src/loom_kernels/ops/attention.py:1-154): same function names,
+argument meaning, default scale ``head_size ** -0.5`` and RuntimeError /
+ValueError behaviour. The tensor contract of the reference's adapter
+(python/csrc/attention.cpp:5-88) is not restated here: the operands go to the
+library as tensor views and its contract tables decide (include/
+loom_hip_views.h), the same code the torch Stable-ABI adapter uses.
 Differences: no 1024-token context cap, and an extended entry point for FP8
 E4M3 caches, HND layouts, log-sum-exp output and fixed split-K partitions.
 
@@ -38,23 +41,40 @@ def _require_inference_tensors(*tensors: torch.Tensor) -> None:
         raise ValueError("Loom Kernels operators are inference-only")
 
 
-def _has_dense_nhd_inner_strides(tensor: torch.Tensor) -> bool:
-    """Only the outer cache-block stride may contain gaps (ops/attention.py:14-26)."""
-    if tensor.dim() != 4:
-        return False
-    _, block_size, heads, width = tensor.shape
-    block_elements = block_size * heads * width
-    return bool(
-        tensor.stride(3) == 1
-        and tensor.stride(2) == width
-        and tensor.stride(1) == heads * width
-        and tensor.stride(0) >= block_elements
-        and tensor.stride(0) <= 0xFFFF_FFFF_FFFF_FFFF
-    )
+_VIEW_DTYPES = {
+    torch.float32: _native.VIEW_F32,
+    torch.float16: _native.VIEW_F16,
+    torch.bfloat16: _native.VIEW_BF16,
+    torch.uint8: _native.VIEW_U8,
+    torch.int32: _native.VIEW_I32,
+    torch.int64: _native.VIEW_I64,
+}
+if getattr(torch, "float8_e4m3fn", None) is not None:
+    _VIEW_DTYPES[torch.float8_e4m3fn] = _native.VIEW_FP8_E4M3FN
 
 
-def _u32(*values: int) -> bool:
-    return all(0 < int(v) <= 0xFFFF_FFFF for v in values)
+def _views(*tensors: torch.Tensor):
+    """The operands as ``loom_hip_tensor_view``s, for the library's contract tables."""
+    views = (_native.TensorView * len(tensors))()
+    for v, t in zip(views, tensors):
+        v.data = t.data_ptr()
+        v.device_index = t.device.index if t.is_cuda else -1
+        v.dtype = _VIEW_DTYPES.get(t.dtype, _native.VIEW_OTHER)
+        v.rank = t.dim()
+        for d in range(min(t.dim(), 5)):
+            v.sizes[d] = t.shape[d]
+            v.strides[d] = t.stride(d)
+    return views
+
+
+def _raise_unless_ok(status: int, operation: str) -> None:
+    """A refused view set raises RuntimeError: the contract's message, or the bridge's."""
+    if status == _native.VIEWS_OK:
+        return
+    message = _native.lib().loom_hip_views_last_error_message().decode()
+    if status == _native.VIEWS_CONTRACT:
+        raise RuntimeError(message)
+    raise _native.LoomHipError(status, f"Loom HIP {operation} bridge failed: {message}")
 
 
 def supports_paged_decode_attention(
@@ -66,65 +86,19 @@ def supports_paged_decode_attention(
     *,
     max_sequence_length: int,
 ) -> bool:
-    """Return whether tensors match the native paged-decode kernel family.
+    """Whether these tensors are accepted by ``paged_decode_attention``.
 
-    Same predicate as ops/attention.py:29-96 without the 1024 context cap.
+    The predicate of python/src/loom_kernels/ops/attention.py:29-96 without
+    its 1024-token cap: the library's decode contract applied to the five
+    inputs (the output and scale rules need the call itself), plus the two
+    facts only Python sees (an ``int`` length, no autograd).
     """
-    if (
-        query.dim() != 3
-        or key_cache.dim() != 4
-        or value_cache.dim() != 4
-        or block_tables.dim() != 2
-        or sequence_lengths.dim() != 1
-        or query.numel() == 0
-        or key_cache.numel() == 0
-        or value_cache.numel() == 0
-        or isinstance(max_sequence_length, bool)
-        or not isinstance(max_sequence_length, int)
-    ):
+    if isinstance(max_sequence_length, bool) or not isinstance(max_sequence_length, int):
         return False
-    sequences, query_heads, head_size = query.shape
-    num_blocks, block_size, kv_heads, key_head_size = key_cache.shape
-    return bool(
-        query.device.type == "cuda"
-        and key_cache.device == query.device
-        and value_cache.device == query.device
-        and block_tables.device == query.device
-        and sequence_lengths.device == query.device
-        and query.dtype in _DTYPE_CODES
-        and key_cache.dtype == query.dtype
-        and value_cache.dtype == query.dtype
-        and block_tables.dtype == torch.int32
-        and sequence_lengths.dtype == torch.int32
-        and query.is_contiguous()
-        and _has_dense_nhd_inner_strides(key_cache)
-        and _has_dense_nhd_inner_strides(value_cache)
-        and block_tables.is_contiguous()
-        and sequence_lengths.is_contiguous()
-        and not query.requires_grad
-        and not key_cache.requires_grad
-        and not value_cache.requires_grad
-        and head_size == key_head_size
-        and value_cache.shape[:3] == (num_blocks, block_size, kv_heads)
-        and value_cache.shape[3] > 0
-        and query_heads % kv_heads == 0
-        and block_tables.shape[0] == sequences
-        and block_tables.shape[1] > 0
-        and sequence_lengths.shape[0] == sequences
-        and 0 < max_sequence_length <= PAGED_DECODE_MAX_CONTEXT
-        and max_sequence_length <= block_tables.shape[1] * block_size
-        and _u32(
-            sequences,
-            query_heads,
-            kv_heads,
-            head_size,
-            value_cache.shape[3],
-            num_blocks,
-            block_size,
-            block_tables.shape[1],
-        )
-        and sequences * query_heads <= 0x7FFF_FFFF
-    )
+    if any(t.requires_grad for t in (query, key_cache, value_cache)):
+        return False
+    views = _views(query, key_cache, value_cache, block_tables, sequence_lengths)
+    return _native.lib().loom_hip_views_paged_decode_check(views, 5, max_sequence_length, 1.0) == _native.VIEWS_OK
 
 
 def _stream_handle(device: torch.device) -> ctypes.c_void_p:
@@ -133,97 +107,6 @@ def _stream_handle(device: torch.device) -> ctypes.c_void_p:
 
 def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if t is None else ctypes.c_void_p(t.data_ptr())
-
-
-def _overlaps(a: torch.Tensor, b: torch.Tensor) -> bool:
-    """Byte-range overlap of the storage spans of two tensors."""
-    def span(t):
-        if t.numel() == 0:
-            return (0, 0)
-        lo = t.data_ptr()
-        hi = lo + (sum((s - 1) * st for s, st in zip(t.shape, t.stride())) + 1) * t.element_size()
-        return (lo, hi)
-
-    a0, a1 = span(a)
-    b0, b1 = span(b)
-    return a0 < b1 and b0 < a1
-
-
-def _check_paged_decode_contract(
-    query, key_cache, value_cache, block_tables, sequence_lengths, output,
-    max_sequence_length, scale,
-) -> None:
-    """python/csrc/attention.cpp:5-87 without the 1024 cap."""
-    def check(cond, msg):
-        if not cond:
-            raise RuntimeError(msg)
-
-    check(query.is_cuda, "Loom paged decode query must be on a GPU")
-    check(
-        key_cache.device == query.device
-        and value_cache.device == query.device
-        and block_tables.device == query.device
-        and sequence_lengths.device == query.device
-        and output.device == query.device,
-        "Loom paged decode tensors must be on one GPU device",
-    )
-    check(query.dtype in _DTYPE_CODES, "Loom paged decode supports F32, FP16, and BF16 native caches")
-    check(
-        key_cache.dtype == query.dtype and value_cache.dtype == query.dtype and output.dtype == query.dtype,
-        "Loom paged decode data tensors must share a dtype",
-    )
-    check(
-        block_tables.dtype == torch.int32 and sequence_lengths.dtype == torch.int32,
-        "Loom paged decode metadata must use int32",
-    )
-    check(
-        query.dim() == 3 and key_cache.dim() == 4 and value_cache.dim() == 4
-        and block_tables.dim() == 2 and sequence_lengths.dim() == 1 and output.dim() == 3,
-        "Loom paged decode requires rank-3 query/output, rank-4 K/V caches, "
-        "rank-2 block tables, and rank-1 sequence lengths",
-    )
-    check(
-        min(query.shape) > 0 and min(key_cache.shape[:3]) > 0 and value_cache.shape[3] > 0,
-        "Loom paged decode dimensions must be positive",
-    )
-    check(key_cache.shape[3] == query.shape[2], "Loom paged decode Q/K head sizes must match")
-    check(value_cache.shape[:3] == key_cache.shape[:3], "Loom paged decode K/V cache prefixes must match")
-    check(query.shape[1] % key_cache.shape[2] == 0, "Loom paged decode query heads must be divisible by KV heads")
-    check(
-        block_tables.shape[0] == query.shape[0] and block_tables.shape[1] > 0
-        and sequence_lengths.shape[0] == query.shape[0],
-        "Loom paged decode metadata batch dimensions must match query",
-    )
-    check(
-        tuple(output.shape) == (query.shape[0], query.shape[1], value_cache.shape[3]),
-        "Loom paged decode output must have shape [B, Hq, Dv]",
-    )
-    check(
-        query.is_contiguous() and _has_dense_nhd_inner_strides(key_cache)
-        and _has_dense_nhd_inner_strides(value_cache) and block_tables.is_contiguous()
-        and sequence_lengths.is_contiguous() and output.is_contiguous(),
-        "Loom paged decode requires contiguous query/output/metadata and "
-        "dense-inner NHD caches with an optional block stride",
-    )
-    check(
-        0 < max_sequence_length <= block_tables.shape[1] * key_cache.shape[1],
-        "Loom paged decode max_sequence_length must be within table capacity",
-    )
-    check(max_sequence_length <= PAGED_DECODE_MAX_CONTEXT, "Loom paged decode shape exceeds the HIP ABI")
-    check(scale == scale and 0.0 < scale < float("inf"), "Loom paged decode scale must be finite and positive")
-    check(
-        not any(_overlaps(output, t) for t in (query, key_cache, value_cache, block_tables, sequence_lengths)),
-        "Loom paged decode output storage must not overlap inputs",
-    )
-    check(
-        _u32(
-            query.shape[0], query.shape[1], key_cache.shape[2], query.shape[2],
-            value_cache.shape[3], key_cache.shape[0], key_cache.shape[1],
-            block_tables.shape[1], max_sequence_length,
-        ),
-        "Loom paged decode shape exceeds the HIP ABI",
-    )
-    check(query.shape[0] * query.shape[1] <= 0x7FFF_FFFF, "Loom paged decode grid exceeds the HIP ABI")
 
 
 def paged_decode_attention_out(
@@ -239,49 +122,31 @@ def paged_decode_attention_out(
 ) -> torch.Tensor:
     """Execute paged decode attention into caller-owned output storage.
 
-    Like the reference adapter (attention.cpp:89-149) this asks the library
-    whether the shape selects split-K, allocates that F32 workspace from the
-    torch allocator when it does, and launches on the current stream.
+    The library checks the views against its decode contract and sizes the
+    split-K workspace; the workspace comes from the torch allocator on the
+    current stream, and the call goes through the checked bridge.
     """
     _require_inference_tensors(query, key_cache, value_cache, output)
     if scale is None:
         scale = query.shape[-1] ** -0.5
-    max_sequence_length = int(max_sequence_length)
-    scale = float(scale)
-    _check_paged_decode_contract(
-        query, key_cache, value_cache, block_tables, sequence_lengths, output,
-        max_sequence_length, scale,
-    )
     lib = _native.lib()
-    code = _DTYPE_CODES[query.dtype]
-    suffix = {_native.F32: "f32", _native.F16: "f16", _native.BF16: "bf16"}[code]
-    sequences, query_heads, head_size = (int(x) for x in query.shape)
-    num_blocks, block_size, kv_heads, _ = (int(x) for x in key_cache.shape)
-    value_head_size = int(value_cache.shape[3])
-    max_blocks = int(block_tables.shape[1])
+    views = _views(query, key_cache, value_cache, block_tables, sequence_lengths, output)
+    max_sequence_length = int(max_sequence_length)
+    elements = ctypes.c_uint64()
+    _raise_unless_ok(
+        lib.loom_hip_views_paged_decode_workspace_elements(views, max_sequence_length, float(scale),
+                                                           ctypes.byref(elements)),
+        "paged decode workspace query",
+    )
     with torch.cuda.device(query.device):
-        stream = _stream_handle(query.device)
-        workspace_elements = lib.loom_hip_paged_decode_attention_split_k_workspace_elements(
-            sequences, query_heads, kv_heads, head_size, value_head_size, max_sequence_length
+        workspace = None
+        if elements.value:
+            workspace = torch.empty(int(elements.value), device=query.device, dtype=torch.float32)
+        _raise_unless_ok(
+            lib.loom_hip_views_paged_decode_attention(views, max_sequence_length, float(scale), _ptr(workspace),
+                                                      elements.value, _stream_handle(query.device)),
+            "paged decode attention",
         )
-        common_tail = (
-            sequences, query_heads, kv_heads, head_size, value_head_size, num_blocks,
-            block_size, key_cache.stride(0), value_cache.stride(0), max_blocks,
-            max_sequence_length, scale, stream,
-        )
-        if workspace_elements:
-            workspace = torch.empty(int(workspace_elements), device=query.device, dtype=torch.float32)
-            status = getattr(lib, f"loom_hip_paged_decode_attention_split_k_{suffix}")(
-                _ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(block_tables),
-                _ptr(sequence_lengths), _ptr(output), _ptr(workspace), workspace_elements,
-                *common_tail,
-            )
-        else:
-            status = getattr(lib, f"loom_hip_paged_decode_attention_{suffix}")(
-                _ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(block_tables),
-                _ptr(sequence_lengths), _ptr(output), *common_tail,
-            )
-    _native.check(status, "Loom paged decode attention")
     return output
 
 
@@ -469,108 +334,13 @@ def supports_rope_paged_kv_write(
 ) -> bool:
     """Whether the tensors match the native/FP8 RoPE+paged-write ABI.
 
-    Same predicate as python/src/loom_kernels/ops/rope_kv.py:11-97.
+    The predicate of python/src/loom_kernels/ops/rope_kv.py:11-97: the
+    library's RoPE+paged-KV contract, plus no autograd on the sources.
     """
-    try:
-        _check_rope_paged_kv_write_contract(
-            query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping
-        )
-    except RuntimeError:
+    if any(t.requires_grad for t in (query, key, value, cos_sin_cache)):
         return False
-    return not any(t.requires_grad for t in (query, key, value, cos_sin_cache))
-
-
-def _kv_span(kv_cache: torch.Tensor, dims: tuple[int, ...]) -> int:
-    return 1 + sum((kv_cache.shape[d] - 1) * kv_cache.stride(d) for d in dims)
-
-
-def _check_rope_paged_kv_write_contract(
-    query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping,
-) -> None:
-    """python/csrc/rope_kv.cpp:37-133 and the ABI limits of :141-150."""
-    def check(cond, msg):
-        if not cond:
-            raise RuntimeError(msg)
-
-    check(query.is_cuda, "Loom RoPE+paged-KV query must be on a GPU")
-    check(
-        all(t.device == query.device for t in (
-            key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping)),
-        "Loom RoPE+paged-KV tensors must be on one GPU device",
-    )
-    check(
-        key.dtype == query.dtype and value.dtype == query.dtype and cos_sin_cache.dtype == query.dtype,
-        "Loom RoPE+paged-KV Q/K/V and cos/sin cache must share a dtype",
-    )
-    check(query.dtype in _DTYPE_CODES, "Loom RoPE+paged-KV supports F32, FP16, and BF16 sources")
-    check(query.dim() == 3 and key.dim() == 3 and value.dim() == 3, "Loom RoPE+paged-KV Q/K/V must have rank 3")
-    check(
-        kv_cache.dtype == query.dtype or kv_cache.dtype == torch.uint8,
-        "Loom paged K/V cache must use the source dtype or uint8 FP8 E4M3 storage",
-    )
-    check(
-        key_scales.dtype == torch.float32 and value_scales.dtype == torch.float32
-        and key_scales.is_contiguous() and value_scales.is_contiguous()
-        and key_scales.numel() == value_scales.numel()
-        and key_scales.numel() in (1, key.shape[1]),
-        "Loom paged K/V cache scales must be contiguous float32 tensors with one element or one element per KV head",
-    )
-    check(
-        positions.dtype == torch.int64 and slot_mapping.dtype == torch.int64,
-        "Loom RoPE+paged-KV positions and slot mapping must be int64",
-    )
-    check(min(query.shape) > 0, "Loom RoPE+paged-KV query must be non-empty")
-    check(
-        key.shape[0] == query.shape[0] and value.shape[0] == query.shape[0],
-        "Loom RoPE+paged-KV Q/K/V token counts must match",
-    )
-    check(key.shape[1] > 0 and key.shape[1] == value.shape[1], "Loom RoPE+paged-KV K/V head counts must match")
-    check(key.shape[2] == query.shape[2], "Loom RoPE+paged-KV Q/K head sizes must match")
-    check(value.shape[2] > 0, "Loom RoPE+paged-KV value head size must be positive")
-    check(
-        query.stride(2) == 1 and key.stride(2) == 1 and value.stride(2) == 1
-        and min(query.stride(0), query.stride(1), key.stride(0), key.stride(1),
-                value.stride(0), value.stride(1)) > 0
-        and positions.is_contiguous() and cos_sin_cache.is_contiguous() and slot_mapping.is_contiguous(),
-        "Loom RoPE+paged-KV sources require unit dim stride and positive token/head strides; "
-        "metadata must be contiguous",
-    )
-    check(
-        positions.dim() == 1 and positions.numel() == query.shape[0]
-        and slot_mapping.dim() == 1 and slot_mapping.numel() <= query.shape[0],
-        "Loom RoPE positions must cover every token and slot_mapping must not exceed the padded token count",
-    )
-    check(
-        cos_sin_cache.dim() == 2 and cos_sin_cache.shape[0] > 0 and cos_sin_cache.shape[1] > 0
-        and cos_sin_cache.shape[1] % 2 == 0 and cos_sin_cache.shape[1] <= query.shape[2],
-        "Loom RoPE+paged-KV cos/sin cache must be [max_position, even rotary_dim <= head_size]",
-    )
-    check(
-        kv_cache.dim() == 5 and kv_cache.shape[1] == 2,
-        "Loom paged K/V cache must have shape [blocks, 2, block_size, kv_heads, head_size]",
-    )
-    check(
-        kv_cache.shape[0] > 0 and kv_cache.shape[2] > 0 and kv_cache.shape[3] == key.shape[1]
-        and kv_cache.shape[4] == key.shape[2] and value.shape[1] == key.shape[1]
-        and value.shape[2] == key.shape[2],
-        "Loom packed K/V cache and K/V sources must share head count and head size",
-    )
-    check(
-        kv_cache.stride(4) == 1 and min(kv_cache.stride()[:4]) > 0,
-        "Loom packed K/V cache requires unit element stride and positive block/KV/page/head strides",
-    )
-    part = _kv_span(kv_cache, (2, 3, 4))
-    check(
-        kv_cache.stride(1) >= part and kv_cache.stride(0) >= kv_cache.stride(1)
-        and kv_cache.stride(0) - kv_cache.stride(1) >= part,
-        "Loom packed K/V cache partitions must not overlap",
-    )
-    check(
-        _u32(query.shape[0], query.shape[1], key.shape[1], query.shape[2], value.shape[2],
-             cos_sin_cache.shape[1], cos_sin_cache.shape[0], kv_cache.shape[0], kv_cache.shape[2])
-        and query.shape[0] <= 0x7FFF_FFFF,
-        "Loom RoPE+paged-KV shape exceeds the HIP ABI",
-    )
+    views = _views(query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping)
+    return _native.lib().loom_hip_views_rope_paged_kv_check(views) == _native.VIEWS_OK
 
 
 def rope_paged_kv_write_(
@@ -587,28 +357,24 @@ def rope_paged_kv_write_(
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Rotate Q/K in place and write native or scaled FP8 E4M3 paged K/V caches.
 
-    Mirrors python/src/loom_kernels/ops/rope_kv.py:100-134 and the adapter
-    python/csrc/rope_kv.cpp:135-220. ``kv_cache`` is
+    Mirrors python/src/loom_kernels/ops/rope_kv.py:100-134. ``kv_cache`` is
     [blocks, 2, block_size, kv_heads, head_size] (K at index 0, V at 1) in the
     source dtype, or uint8 holding FP8 E4M3FN bytes. Scale tensors are always
     passed; native caches ignore them, FP8 caches index them per tensor (one
     element) or per KV head. ``slot_mapping`` covers the first
-    ``slot_mapping.numel()`` tokens; negative slots are padding. Returns
+    ``slot_mapping.numel()`` tokens; negative slots are padding. The library
+    checks the views and submits through the checked bridge. Returns
     ``(query, key, kv_cache)``.
     """
     _require_inference_tensors(query, key, value, cos_sin_cache, kv_cache, key_scales, value_scales)
-    _check_rope_paged_kv_write_contract(
-        query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping
-    )
-    value_cache = kv_cache[:, 1]
-    block, page, head = kv_cache.stride(0), kv_cache.stride(2), kv_cache.stride(3)
-    rope_paged_kv_write_strided(
-        query, key, value, positions, cos_sin_cache, kv_cache[:, 0], value_cache,
-        key_scales, value_scales, slot_mapping,
-        num_blocks=int(kv_cache.shape[0]), block_size=int(kv_cache.shape[2]),
-        key_cache_strides=(block, page, head), value_cache_strides=(block, page, head),
-        scale_stride=0 if key_scales.numel() == 1 else 1, is_neox=is_neox,
-    )
+    views = _views(query, key, value, positions, cos_sin_cache, kv_cache, key_scales, value_scales, slot_mapping)
+    lib = _native.lib()
+    _raise_unless_ok(lib.loom_hip_views_rope_paged_kv_check(views), "RoPE+paged-KV")
+    with torch.cuda.device(query.device):
+        _raise_unless_ok(
+            lib.loom_hip_views_rope_paged_kv_write(views, 1 if is_neox else 0, _stream_handle(query.device)),
+            "RoPE+paged-KV",
+        )
     return query, key, kv_cache
 
 

@@ -19,7 +19,7 @@ import torch
 from attnarc_amd import _native, ops
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("loom_hip.h", "loom_hip_bridge.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("loom_hip.h", "loom_hip_bridge.h", "loom_hip_views.h")]
 
 
 def declared_functions():
