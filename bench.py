@@ -82,43 +82,18 @@ def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
     return moved / sec / 1e9
 
 
-def gather_probe(chunk_bytes: int, total_bytes: int = 2 << 30, iters: int = 10, per_cu: int = 16,
-                 unroll: int = 8) -> float:
-    """Bandwidth of reading ``total_bytes`` as randomly permuted chunks of
-    ``chunk_bytes`` (the granularity of a paged K/V access pattern)."""
-    import ctypes
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
 
-    import torch
-
-    from attnarc_amd import build as _b
-
-    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
-    lib.loom_hip_probe_gather_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
-                                               ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
-    chunks = total_bytes // chunk_bytes
-    base = torch.empty(total_bytes // 4, dtype=torch.int32, device="cuda").fill_(3)
-    g = torch.Generator(device="cuda")
-    g.manual_seed(7)
-    perm = torch.randperm(chunks, generator=g, device="cuda").to(torch.int32)
-    blocks = torch.cuda.get_device_properties(0).multi_processor_count * per_cu
-    sink = torch.empty(blocks * 256, dtype=torch.int32, device="cuda")
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-    def once():
-        rc = lib.loom_hip_probe_gather_read(base.data_ptr(), perm.data_ptr(), chunks, chunk_bytes,
-                                            sink.data_ptr(), blocks, unroll, stream)
-        assert rc == 0, rc
-
-    once()
-    torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(iters):
-        once()
-    b.record()
-    torch.cuda.synchronize()
-    return total_bytes / (a.elapsed_time(b) / iters * 1e-3) / 1e9
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(case, budget_s: float = 15.0):
@@ -127,7 +102,7 @@ def cpu_baseline(case, budget_s: float = 15.0):
 
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle
-    from gpu_util import to_host
+    from gpu_util import ORACLE_DTYPE, to_host
 
     oracle.lib()
     kc = to_host(case.key_cache)
@@ -135,21 +110,27 @@ def cpu_baseline(case, budget_s: float = 15.0):
     q = to_host(case.query)
     tables = to_host(case.block_tables).astype(np.int64)
     lens = to_host(case.sequence_lengths).astype(np.int64)
-    kl = oracle.CacheLayout.nhd(case.block_size, case.kv_heads, case.head_size)
-    vl = oracle.CacheLayout.nhd(case.block_size, case.kv_heads, case.value_head_size)
-    # calibrate on one sequence, then size the sample to the budget
+    layout = oracle.CacheLayout.nhd if case.layout == "NHD" else oracle.CacheLayout.hnd
+    kl = layout(case.block_size, case.kv_heads, case.head_size)
+    vl = layout(case.block_size, case.kv_heads, case.value_head_size)
+    extra = {}
+    if case.cache_encoding == "fp8":
+        extra = dict(cache_encoding=oracle.FP8_E4M3, key_scales=case.key_scales.cpu().numpy(),
+                     value_scales=case.value_scales.cpu().numpy(),
+                     scale_stride=1 if case.key_scales.numel() > 1 else 0)
+    # one sequence at a time until the budget is spent
     done_bytes = 0
     elapsed = 0.0
     used = 0
     for s in range(case.sequences):
         spec = oracle.spec_new(1, case.query_heads, case.kv_heads, case.head_size, case.value_head_size,
                                case.num_blocks, case.block_size, case.max_blocks_per_sequence, int(lens[s]),
-                               case.scale, oracle.BF16)
+                               case.scale, ORACLE_DTYPE[case.dtype])
         t0 = time.perf_counter()
         oracle.ext(spec, np.ascontiguousarray(q[s:s + 1]), kc, vc, np.ascontiguousarray(tables[s:s + 1]),
-                   lens[s:s + 1], key_layout=kl, value_layout=vl, want_lse=False)
+                   lens[s:s + 1], key_layout=kl, value_layout=vl, want_lse=False, **extra)
         elapsed += time.perf_counter() - t0
-        done_bytes += int(lens[s]) * case.kv_heads * (case.head_size + case.value_head_size) * 2
+        done_bytes += int(lens[s]) * case.kv_heads * (case.head_size + case.value_head_size) * case.kv_elem_bytes
         used += 1
         if elapsed >= budget_s:
             break
@@ -158,9 +139,11 @@ def cpu_baseline(case, budget_s: float = 15.0):
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
         "sample": f"first {used} of {case.sequences} sequences of the same workload "
                   f"({sum(case.lengths[:used])} tokens, {elapsed:.1f} s, single-threaded C++ oracle, "
-                  f"F64 two-pass; host nproc={os.cpu_count()})",
+                  f"F64 two-pass) on {cpu_model()}",
         "seconds_per_call_extrapolated": elapsed * sum(case.lengths) / max(1, sum(case.lengths[:used])),
     }
 
@@ -220,8 +203,10 @@ def rope_cpu_baseline(case, budget_s: float):
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
         "sample": f"first {n} of {t} tokens of the same workload ({elapsed:.1f} s, single-threaded C++ oracle, "
-                  f"cache-copy time excluded; host nproc={os.cpu_count()})",
+                  f"cache-copy time excluded) on {cpu_model()}",
     }
 
 
@@ -439,7 +424,7 @@ def main() -> int:
     ap.add_argument("--shape", default=None,
                     help="a decode workload other than the five configurations, e.g. "
                          "'B=64,Hq=16,Hkv=8,D=256,L=2048,part=512' (see workloads.shape_case); not the metric")
-    ap.add_argument("--probe", choices=["read", "copy", "gather"], default=None,
+    ap.add_argument("--probe", choices=["read", "copy"], default=None,
                     help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
 
@@ -459,13 +444,6 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.probe == "gather":
-        for cb in (256, 4096):
-            for per_cu, unroll in ((16, 8), (8, 8), (4, 8), (2, 8), (2, 16), (2, 32), (1, 32)):
-                bw = gather_probe(cb, per_cu=per_cu, unroll=unroll)
-                print(json.dumps({"probe": "gather", "chunk_bytes": cb, "waves_per_cu": per_cu * 4,
-                                  "kib_in_flight_per_wave": unroll, "GB/s": round(bw, 1)}), flush=True)
-        return 0
     if args.probe:
         print(json.dumps({"probe": args.probe, "bytes": 4 << 30, "GB/s": round(hbm_probe(args.probe), 1)}))
         return 0

@@ -17,6 +17,9 @@ TOL = {
 }
 LSE_TOL = dict(atol=1e-4, rtol=1e-5)
 
+# Host threads for full-size oracle runs (the GPU box gives a job 16 CPUs).
+ORACLE_THREADS = 16
+
 
 def to_host(t: torch.Tensor) -> np.ndarray:
     """Bit-exact host copy: BF16 as uint16, F16 as float16, FP8 as uint8."""
@@ -38,13 +41,33 @@ def as_f64(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def oracle_expected(case, seqs=None):
+def oracle_expected(case, seqs=None, threads=None, _host_caches=None):
     """Oracle output (F64 of the dtype-rounded result) and LSE for a DecodeCase.
 
     ``seqs`` restricts the oracle to a subset of sequences (the caches are
-    shared, so only Q, tables and lengths are sliced).
+    shared, so only Q, tables and lengths are sliced). With ``threads`` > 1
+    the sequences are split into that many groups run concurrently (ctypes
+    releases the GIL); each group is the same single-threaded oracle, so the
+    result is identical to one call.
     """
     idx = list(range(case.sequences)) if seqs is None else list(seqs)
+    if threads and threads > 1 and len(idx) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        # Longest sequences first, dealt round-robin, so the groups take similar time.
+        order = sorted(idx, key=lambda i: -case.lengths[i])
+        groups = [sorted(order[g::threads]) for g in range(min(threads, len(idx)))]
+        with ThreadPoolExecutor(len(groups)) as pool:
+            caches = (to_host(case.key_cache), to_host(case.value_cache))
+            parts = list(pool.map(lambda g: oracle_expected(case, g, _host_caches=caches), groups))
+        out = np.empty((len(idx), case.query_heads, case.value_head_size), dtype=np.float64)
+        lse = np.empty((len(idx), case.query_heads), dtype=np.float64)
+        pos = {s: k for k, s in enumerate(idx)}
+        for g, (o, l) in zip(groups, parts):
+            rows = [pos[s] for s in g]
+            out[rows] = o
+            lse[rows] = l
+        return out, lse
     q = case.query[idx]
     tables = case.block_tables[idx]
     lens = case.sequence_lengths[idx]
@@ -54,8 +77,7 @@ def oracle_expected(case, seqs=None):
         len(idx), case.query_heads, case.kv_heads, case.head_size, case.value_head_size, case.num_blocks,
         case.block_size, case.max_blocks_per_sequence, max(lengths), case.scale, dt,
     )
-    kc = to_host(case.key_cache)
-    vc = to_host(case.value_cache)
+    kc, vc = _host_caches if _host_caches is not None else (to_host(case.key_cache), to_host(case.value_cache))
     if case.layout == "NHD":
         kl = oracle.CacheLayout.nhd(case.block_size, case.kv_heads, case.head_size)
         vl = oracle.CacheLayout.nhd(case.block_size, case.kv_heads, case.value_head_size)

@@ -20,7 +20,7 @@ import torch
 
 import oracle
 from attnarc_amd import ops, workloads
-from gpu_util import LSE_TOL, assert_parity, as_f64, oracle_expected
+from gpu_util import LSE_TOL, ORACLE_THREADS, assert_parity, as_f64, oracle_expected
 
 pytestmark = pytest.mark.gpu
 
@@ -438,14 +438,16 @@ def test_config2_single_partition_full():
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
-@pytest.mark.parametrize("index,subset", [(3, [0, 17, 40, 63]), (4, [0, 77]), (5, [3])])
-def test_config_subset_against_oracle_and_split_invariance(index, subset):
+@pytest.mark.parametrize("index", [3, 4, 5])
+def test_config_full_against_oracle_and_split_invariance(index):
+    """Every sequence of C3, C4 and C5 against the oracle (threaded over
+    sequences), then split-K invariance over other partition sizes."""
     case = workloads.config(index, DEV)
     out, lse = workloads.run_case(case, return_lse=True)
     torch.cuda.synchronize()
-    expected, want_lse = oracle_expected(case, subset)
-    assert_parity(out[subset], expected, case.dtype, f"c{index} subset")
-    np.testing.assert_allclose(lse[subset].cpu().numpy(), want_lse, **LSE_TOL)
+    expected, want_lse = oracle_expected(case, threads=ORACLE_THREADS)
+    assert_parity(out, expected, case.dtype, f"c{index} full")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
     # Size-independent property over every sequence: one partition per
     # sequence and a different partition size give the same result.
     for other in (0, 3 * case.partition_tokens // 2 + 16):
