@@ -13,8 +13,13 @@ import threading
 
 from . import build as _build
 
-# LOOM_HIP_LIBRARY selects another build of the same ABI (e.g. for A/B runs).
+# LOOM_HIP_LIBRARY selects another build of the same ABI (A/B runs, the
+# profiling build); it is read when the library is first loaded.
 LIB_PATH = os.environ.get("LOOM_HIP_LIBRARY", _build.LIB_PATH)
+
+
+def library_path() -> str:
+    return os.environ.get("LOOM_HIP_LIBRARY", _build.LIB_PATH)
 
 SUCCESS = 0
 INVALID_ARGUMENT = 1
@@ -134,6 +139,8 @@ def lib() -> ctypes.CDLL:
         return _lib
     with _lock:
         if _lib is None:
+            global LIB_PATH
+            LIB_PATH = library_path()
             if not os.path.exists(LIB_PATH):
                 raise ImportError(
                     f"loom-hip native library not found at {LIB_PATH}; "

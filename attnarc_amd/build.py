@@ -96,6 +96,25 @@ def _compile_adapter(verbose: bool) -> None:
     os.replace(tmp, ADAPTER_LIB_PATH)
 
 
+WAVE_TRACE_LIB_PATH = os.path.join(PKG_DIR, "_build", "libloom_hip_wave_trace.so")
+
+
+def build_wave_trace(verbose: bool = False) -> str:
+    """The profiling build of the library with per-wave timeline records
+    (-DLOOM_HIP_WAVE_TRACE), used by ``attnarc_amd.wave_trace``; the other
+    objects are the regular ones."""
+    build(verbose=verbose, incremental=True)
+    obj_dir = os.path.join(os.path.dirname(LIB_PATH), "obj")
+    traced = os.path.join(obj_dir, "paged_decode_attention_wave_trace.o")
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    _run([HIPCC, *flags, "-DLOOM_HIP_WAVE_TRACE", "-c", SOURCES[0], "-o", traced], verbose)
+    others = [os.path.join(obj_dir, os.path.basename(src) + ".o") for src in SOURCES[1:]]
+    tmp = WAVE_TRACE_LIB_PATH + ".tmp"
+    _run([HIPCC, *HIPCC_FLAGS, traced, *others, "-o", tmp], verbose)
+    os.replace(tmp, WAVE_TRACE_LIB_PATH)
+    return WAVE_TRACE_LIB_PATH
+
+
 def build(verbose: bool = False, incremental: bool = False) -> str:
     """Compile the kernel library, the HBM probe library and the torch adapter; returns the first's path."""
     _compile(SOURCES, LIB_PATH, verbose, incremental)
@@ -107,4 +126,7 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
 if __name__ == "__main__":
     import sys
 
-    print(build(verbose=True, incremental="--incremental" in sys.argv))
+    if "--wave-trace" in sys.argv:
+        print(build_wave_trace(verbose=True))
+    else:
+        print(build(verbose=True, incremental="--incremental" in sys.argv))

@@ -49,3 +49,31 @@ extern "C" int loom_hip_probe_copy(const void* src, void* dst, uint64_t bytes, u
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
+// Contiguous-slice read: workgroup b of `blocks` reads bytes [b * bytes / blocks,
+// (b + 1) * bytes / blocks), eight 16-byte loads per thread in flight. With
+// one workgroup on each of n CUs it measures what n CUs can pull (a
+// single-partition decode over n work items uses n CUs).
+__global__ __launch_bounds__(512) void slice_read_kernel(const u32x4* __restrict__ src, uint64_t n16_per_block,
+                                                         uint32_t* __restrict__ sink) {
+  const u32x4* p = src + static_cast<uint64_t>(blockIdx.x) * n16_per_block;
+  u32x4 acc = {0U, 0U, 0U, 0U};
+  for (uint64_t i = threadIdx.x; i < n16_per_block; i += 8ULL * blockDim.x) {
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint64_t j = i + static_cast<uint64_t>(k) * blockDim.x;
+      v[k] = j < n16_per_block ? __builtin_nontemporal_load(&p[j]) : u32x4{0U, 0U, 0U, 0U};
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc ^= v[k];
+  }
+  sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
+extern "C" int loom_hip_probe_slice_read(const void* src, uint64_t bytes, uint32_t* sink, uint32_t blocks,
+                                         void* stream) {
+  if (src == nullptr || sink == nullptr || blocks == 0 || bytes % (16ULL * blocks) != 0) return 1;
+  hipLaunchKernelGGL(slice_read_kernel, dim3(blocks), dim3(512), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src), bytes / 16 / blocks, sink);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}

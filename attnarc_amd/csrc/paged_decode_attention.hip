@@ -1558,6 +1558,48 @@ struct StreamDecoder {
   }
 };
 
+// Per-wave timeline of the streaming kernels, compiled only into profiling
+// builds (-DLOOM_HIP_WAVE_TRACE, attnarc_amd/wave_trace.py): each wave of an
+// item records its start and end (s_memrealtime, 100 MHz), XCC and hardware
+// IDs, and the item. The record of wave slot i of a launch goes to entry i.
+#ifdef LOOM_HIP_WAVE_TRACE
+struct WaveRecord {
+  unsigned long long t0, t1;
+  uint32_t xcc, hw_id, seq, part, kvh, tokens;
+};
+constexpr uint32_t kWaveRecords = 1U << 16;
+__device__ WaveRecord g_wave_records[kWaveRecords];
+
+struct WaveStamp {
+  uint32_t slot;
+  unsigned long long t0;
+  uint32_t seq = 0, part = 0, kvh = 0, tokens = 0;
+  __device__ ~WaveStamp() {
+    const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+    uint32_t xcc, hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    if ((threadIdx.x & 63U) == 0 && slot < kWaveRecords && tokens != 0)
+      g_wave_records[slot] = WaveRecord{t0, t1, xcc, hw, seq, part, kvh, tokens};
+  }
+};
+#define LOOM_WAVE_STAMP(slot) WaveStamp wave_stamp{(slot), __builtin_amdgcn_s_memrealtime()}
+#define LOOM_WAVE_ITEM(a, item)                                                                            \
+  do {                                                                                                     \
+    wave_stamp.seq = (item).seq;                                                                           \
+    wave_stamp.part = (item).part;                                                                         \
+    wave_stamp.kvh = (item).kvh;                                                                           \
+    wave_stamp.tokens = (item).valid ? min((item).len - (item).part * (a).partition_tokens, (a).partition_tokens) : 0U; \
+  } while (0)
+#else
+#define LOOM_WAVE_STAMP(slot) \
+  do {                        \
+  } while (0)
+#define LOOM_WAVE_ITEM(a, item) \
+  do {                          \
+  } while (0)
+#endif
+
 // Work-item schedule of the streaming kernel. The grid has one workgroup per
 // (sequence, partition, KV head) slot; slots are handed out so that every full
 // partition comes first and the shorter last partitions of the sequences come
@@ -2021,7 +2063,9 @@ __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2))
 void decode_stream_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8, kHT, kD>;
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kSplit * Dec::kWaveBytes];
+  LOOM_WAVE_STAMP(blockIdx.x * kSplit + (threadIdx.x >> 6));
   const WorkItem item = schedule_item(a, blockIdx.x);
+  LOOM_WAVE_ITEM(a, item);
   if (!item.valid) return;  // uniform across the workgroup
   stream_item<QE, kFp8, kSplit, kHT, kD>(a, tiles, item);
 }
@@ -2047,10 +2091,13 @@ void decode_stream_group_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8, 1, kD>;
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * Dec::kWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  LOOM_WAVE_STAMP(blockIdx.x * kGroup + wave);
   const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
+  LOOM_WAVE_ITEM(a, item);
   if (!item.valid) return;  // per wave: nothing below waits on the other waves
   stream_item<QE, kFp8, 1, 1, kD>(a, tiles + wave * Dec::kWaveBytes, item);
 }
+
 
 // Groups of 33-128 query heads: one workgroup of ceil(group / 32) waves per
 // work item (stream_item_shared), so that each K/V row is read from HBM once
@@ -3514,3 +3561,17 @@ int loom_hip_paged_decode_attention_extended_no_alloc(
 }
 
 }  // extern "C"
+
+#ifdef LOOM_HIP_WAVE_TRACE
+// Profiling builds only (not part of the ABI): copies the wave records of the
+// launches so far to host memory and clears them.
+extern "C" int loom_hip_wave_trace_read(void* host, uint64_t bytes) {
+  const uint64_t n = bytes < sizeof(g_wave_records) ? bytes : sizeof(g_wave_records);
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(g_wave_records), n, 0, hipMemcpyDeviceToHost) != hipSuccess) return 1;
+  static WaveRecord zero[1024];
+  for (uint64_t off = 0; off < sizeof(g_wave_records); off += sizeof(zero))
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_wave_records), zero, sizeof(zero), off, hipMemcpyHostToDevice) != hipSuccess)
+      return 1;
+  return 0;
+}
+#endif

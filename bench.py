@@ -82,6 +82,36 @@ def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
     return moved / sec / 1e9
 
 
+def slice_probe(workgroups: int, nbytes: int = 64 << 20, copies: int = 16, iters: int = 20) -> float:
+    """Read rate of ``workgroups`` 512-thread workgroups (one per CU), each
+    streaming a contiguous slice; ``copies`` rotated buffers keep the reads out
+    of the Infinity Cache."""
+    import ctypes
+
+    import torch
+
+    from attnarc_amd import build as _b
+
+    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
+    lib.loom_hip_probe_slice_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint32,
+                                              ctypes.c_void_p]
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(copies)]
+    sink = torch.empty(workgroups * 512, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nb = nbytes - nbytes % (16 * workgroups)
+    for i in range(copies):
+        assert lib.loom_hip_probe_slice_read(bufs[i].data_ptr(), nb, sink.data_ptr(), workgroups, stream) == 0
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(iters):
+        assert lib.loom_hip_probe_slice_read(bufs[i % copies].data_ptr(), nb, sink.data_ptr(), workgroups, stream) == 0
+    b.record()
+    torch.cuda.synchronize()
+    return nb * iters / (a.elapsed_time(b) * 1e-3) / 1e9
+
+
 def cpu_model() -> str:
     """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
     try:
@@ -424,7 +454,7 @@ def main() -> int:
     ap.add_argument("--shape", default=None,
                     help="a decode workload other than the five configurations, e.g. "
                          "'B=64,Hq=16,Hkv=8,D=256,L=2048,part=512' (see workloads.shape_case); not the metric")
-    ap.add_argument("--probe", choices=["read", "copy"], default=None,
+    ap.add_argument("--probe", choices=["read", "copy", "slice"], default=None,
                     help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
 
@@ -444,6 +474,11 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.probe == "slice":
+        for wgs in (64, 128, 256, 512):
+            print(json.dumps({"probe": "slice", "workgroups": wgs, "threads": 512, "bytes": 64 << 20,
+                              "GB/s": round(slice_probe(wgs), 1)}), flush=True)
+        return 0
     if args.probe:
         print(json.dumps({"probe": args.probe, "bytes": 4 << 30, "GB/s": round(hbm_probe(args.probe), 1)}))
         return 0
