@@ -2398,6 +2398,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
 // Host side: error reporting, telemetry, validation, planning, launch.
 // ---------------------------------------------------------------------------
 thread_local std::string g_last_error;
+thread_local const char* g_last_family = "";
 std::atomic<uint64_t> g_decode_launches{0};
 std::atomic<uint64_t> g_rope_launches{0};
 
@@ -2608,6 +2609,13 @@ int validate(const Problem& p) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
 
+// The matrix-core kernels store the output (and 16-bit partial states) four
+// 16-bit elements at a time with 8-byte stores.
+bool stores_aligned8(const Problem& p) {
+  const auto a8 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7U) == 0; };
+  return a8(p.output) && (p.workspace == nullptr || a8(p.workspace));
+}
+
 // Shape-level eligibility of the matrix-core kernel.
 bool mfma_shape(uint32_t dtype, uint32_t head_size, uint32_t value_head_size,
                 uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
@@ -2623,7 +2631,7 @@ bool mfma_eligible(const Problem& p) {
   for (uint64_t s : strides) {
     if ((s * es) % 16 != 0) return false;
   }
-  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache);
+  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) && stores_aligned8(p);
 }
 
 uint32_t log2u(uint32_t v) {
@@ -2753,7 +2761,7 @@ bool heads_stream_eligible(const Problem& p, uint64_t parts) {
   }
   if (parts > 1 && p.partition_tokens % kStep != 0) return false;
   const uint64_t limit = 1ULL << 31;
-  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) &&
+  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) && stores_aligned8(p) &&
          15 * p.k_page * es + 256 < limit && 15 * p.v_page * es + 256 < limit;
 }
 
@@ -2786,7 +2794,8 @@ bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   for (uint64_t st : strides) {
     if ((st * es) % 16 != 0) return false;
   }
-  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) && stream_eligible(p, parts, group);
+  return aligned16(p.query) && aligned16(p.key_cache) && aligned16(p.value_cache) && stores_aligned8(p) &&
+         stream_eligible(p, parts, group);
 }
 
 
@@ -3001,6 +3010,9 @@ int run_typed(const Problem& p, hipStream_t stream) {
                  : launch_vector<QE, QE>(args, grid, stream);
   }
   if (status != LOOM_HIP_SUCCESS) return fail(status, "decode kernel launch failed");
+  g_last_family = use_heads || use_narrow ? "mfma-stream"
+                  : use_mfma             ? (stream_eligible(p, parts, group) ? "mfma-stream" : "mfma")
+                                         : "vector";
   if (parts > 1) {
     status = launch_merge<QE>(args, p.sequences * p.query_heads, stream);
     if (status != LOOM_HIP_SUCCESS) return fail(status, "merge kernel launch failed");
@@ -3252,6 +3264,8 @@ const char* loom_hip_backend_name(void) { return "loom-hip"; }
 uint32_t loom_hip_abi_version(void) { return 1; }
 
 const char* loom_hip_last_error_message(void) { return g_last_error.c_str(); }
+
+const char* loom_hip_last_kernel_family(void) { return g_last_family; }
 
 int loom_hip_launch_count(uint32_t operation, uint64_t* count) {
   if ((operation != LOOM_HIP_PAGED_DECODE_ATTENTION && operation != LOOM_HIP_ROPE_PAGED_KV_WRITE) ||

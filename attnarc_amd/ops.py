@@ -451,6 +451,11 @@ def supports(
     return status, reason.value.decode(), family.value.decode()
 
 
+def last_kernel_family() -> str:
+    """Kernel family the last successful paged-decode call on this thread launched."""
+    return _native.lib().loom_hip_last_kernel_family().decode()
+
+
 def launch_count(operation: int = _native.PAGED_DECODE_ATTENTION) -> int:
     count = ctypes.c_uint64()
     _native.check(_native.lib().loom_hip_launch_count(operation, ctypes.byref(count)), "launch count")

@@ -358,6 +358,16 @@ uint32_t loom_hip_abi_version(void);
 const char* loom_hip_last_error_message(void);
 
 /*
+ * Kernel family ("mfma-stream", "mfma" or "vector", the names of
+ * loom_hip_paged_decode_attention_supports) that the last successful paged
+ * decode call on this thread launched; "" before the first. No reference
+ * counterpart: a diagnostic for tests and profiling, since the family also
+ * depends on pointer and stride alignment and the partition size, which the
+ * capability query does not see.
+ */
+const char* loom_hip_last_kernel_family(void);
+
+/*
  * Relaxed atomic launch counters (replace loom_cuda_bridge_launch_count /
  * _reset_launch_count, cuda/mod.rs:733-774). One successful decode call
  * counts once regardless of how many kernels it launches.

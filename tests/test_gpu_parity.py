@@ -261,9 +261,36 @@ def test_matrix_core_kernels_match_oracle(dtype, encoding, block_size, partition
     case = case_from(shape, dtype, seed=23, cache_encoding=encoding, layout="NHD",
                      partition_tokens=partition_tokens)
     out, lse = workloads.run_case(case, return_lse=True)
+    assert ops.last_kernel_family() == family
     torch.cuda.synchronize()
     expected, want_lse = oracle_expected(case)
     assert_parity(out, expected, dtype, f"{family} bs{block_size} part{partition_tokens} {encoding}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
+@pytest.mark.parametrize("partition_tokens,misaligned", [(512, "output"), (0, "output"), (512, "workspace")])
+def test_unaligned_output_or_workspace_takes_the_vector_kernel(partition_tokens, misaligned):
+    """The matrix-core kernels store four 16-bit elements at a time (8 bytes):
+    an output view or a workspace that is only element-aligned runs on the
+    general kernel, with the same results."""
+    shape = (4, 32, 8, 128, 128, 16, [700, 1, 33, 2050])
+    case = case_from(shape, torch.bfloat16, seed=29, partition_tokens=partition_tokens)
+    expected, want_lse = oracle_expected(case)
+    aligned = workloads.run_case(case)
+    assert ops.last_kernel_family() == "mfma-stream"
+    out = None
+    workspace = None
+    if misaligned == "output":
+        store = torch.empty(aligned.numel() + 1, device=DEV, dtype=torch.bfloat16)
+        out = store[1:].view(aligned.shape)  # 2-byte aligned
+    else:
+        need = ops.extended_workspace_elements(case.sequences, case.query_heads, case.value_head_size,
+                                               case.max_sequence_length, partition_tokens)
+        workspace = torch.empty(need + 1, device=DEV, dtype=torch.float32)[1:]  # 4-byte aligned
+    got, lse = workloads.run_case(case, output=out, workspace=workspace, return_lse=True)
+    assert ops.last_kernel_family() == "vector"
+    torch.cuda.synchronize()
+    assert_parity(got, expected, torch.bfloat16, f"unaligned {misaligned}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
