@@ -2312,12 +2312,16 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
 
 // Split-K merge, latency path for the common shape: 16-bit partials, Dv = 128,
 // at most 256 partitions (partial rows of 256 bytes, 16-byte aligned). One
-// workgroup of 256 threads per row; thread (g, c) owns dims 8c..8c+7 of
-// partitions g, g + 16, ... All of a row's partial loads and its (m, l) loads
-// are issued at the start, so the row costs one memory round trip; the
-// weights w_p = 2^(m_p - M) l_p and L = sum w_p come from two block
-// reductions while the partials are in flight, and the 16 partition groups
-// are summed in LDS.
+// workgroup of 256 threads per row, merging in two stages of the log-sum-exp
+// identity. Thread (g, c) owns dims 8c..8c+7 of the partitions of group g
+// (partitions g, g + 16, ...). All of a row's partial and (m, l) loads are
+// issued at the start, so the row costs one memory round trip.
+//   Stage 1 (registers): each group's state (M_g, L_g, O_g) from its own
+//     maximum, M_g = max m_p, L_g = sum 2^(m_p - M_g) l_p, O_g = sum
+//     2^(m_p - M_g) l_p o_p (o_p is the stored O_p / l_p).
+//   Stage 2 (LDS, one barrier): M = max M_g, L = sum 2^(M_g - M) L_g,
+//     out = sum 2^(M_g - M) O_g / L.
+// A group without partitions has M_g = -inf and weight 0.
 constexpr uint32_t kMergeFastParts = 256;
 constexpr uint32_t kMergeFastDim = 128;
 
@@ -2326,9 +2330,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
   using QT = typename QE::T;
   constexpr uint32_t kGroups = kMergeThreads / 16;            // partition groups
   constexpr uint32_t kPerThread = kMergeFastParts / kGroups;  // partitions per thread
-  __shared__ float wgt[kMergeFastParts];
-  __shared__ float red[kMergeWaves];
   __shared__ float part[kGroups][kMergeFastDim + 4];
+  __shared__ float group_ml[kGroups][2];
   const uint32_t row = blockIdx.x;
   const uint32_t seq = row / a.query_heads;
   const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
@@ -2339,42 +2342,31 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
   const float* ml = a.ws_ml + s0 * 2;
   const uint16_t* os = static_cast<const uint16_t*>(a.ws_o) + s0 * kMergeFastDim;
   const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid & 63U;
-  const uint32_t wave = tid >> 6;
   const uint32_t c = tid & 15U;
   const uint32_t g = tid >> 4;
 
   uint4 ov[kPerThread];
+  float mp[kPerThread], lp[kPerThread];
 #pragma unroll
   for (uint32_t i = 0; i < kPerThread; ++i) {
     const uint32_t p = g + kGroups * i;
-    ov[i] = p < n ? *reinterpret_cast<const uint4*>(os + static_cast<uint64_t>(p) * sstride * kMergeFastDim + 8 * c)
-                  : make_uint4(0U, 0U, 0U, 0U);
+    const bool live = p < n;
+    ov[i] = live ? *reinterpret_cast<const uint4*>(os + static_cast<uint64_t>(p) * sstride * kMergeFastDim + 8 * c)
+                 : make_uint4(0U, 0U, 0U, 0U);
+    mp[i] = live ? ml[2 * sstride * p] : -INFINITY;
+    lp[i] = live ? ml[2 * sstride * p + 1] : 0.0f;
   }
-  const float m = tid < n ? ml[2 * sstride * tid] : -INFINITY;
-  const float lp = tid < n ? ml[2 * sstride * tid + 1] : 0.0f;
 
-  float M = wave_max_dpp(m);
-  if (lane == 0) red[wave] = M;
-  __syncthreads();
-  M = red[0];
+  // Stage 1: this group's partitions.
+  float Mg = -INFINITY;
 #pragma unroll
-  for (uint32_t w = 1; w < kMergeWaves; ++w) M = fmaxf(M, red[w]);
-  __syncthreads();
-  const float w = tid < n ? exp2f(m - M) * lp : 0.0f;  // weight of the stored O_p / l_p
-  wgt[tid] = w;
-  const float ws = wave_sum_dpp(w);
-  if (lane == 0) red[wave] = ws;
-  __syncthreads();
-  float L = 0.0f;
-#pragma unroll
-  for (uint32_t v = 0; v < kMergeWaves; ++v) L += red[v];
-
+  for (uint32_t i = 0; i < kPerThread; ++i) Mg = fmaxf(Mg, mp[i]);
+  float Lg = 0.0f;
   float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (uint32_t i = 0; i < kPerThread; ++i) {
-    const uint32_t p = g + kGroups * i;
-    const float f = p < n ? wgt[p] : 0.0f;
+    const float f = g + kGroups * i < n ? exp2f(mp[i] - Mg) * lp[i] : 0.0f;  // weight of the stored O_p / l_p
+    Lg += f;
     const uint32_t words[4] = {ov[i].x, ov[i].y, ov[i].z, ov[i].w};
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
@@ -2384,14 +2376,27 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
   }
 #pragma unroll
   for (uint32_t j = 0; j < 8; ++j) part[g][8 * c + j] = acc[j];
-  __syncthreads();
-  if (tid < kMergeFastDim) {
-    float O = 0.0f;
-#pragma unroll
-    for (uint32_t v = 0; v < kGroups; ++v) O += part[v][tid];
-    static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * kMergeFastDim + tid] = QE::from_f(O / L);
+  if (c == 0) {
+    group_ml[g][0] = Mg;
+    group_ml[g][1] = Lg;
   }
-  if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
+  __syncthreads();
+
+  // Stage 2: the group states.
+  float M = -INFINITY;
+#pragma unroll
+  for (uint32_t v = 0; v < kGroups; ++v) M = fmaxf(M, group_ml[v][0]);
+  if (tid < kMergeFastDim) {
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (uint32_t v = 0; v < kGroups; ++v) {
+      const float f = isfinite(group_ml[v][0]) ? exp2f(group_ml[v][0] - M) : 0.0f;
+      L = fmaf(group_ml[v][1], f, L);
+      O = fmaf(part[v][tid], f, O);
+    }
+    static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * kMergeFastDim + tid] = QE::from_f(O / L);
+    if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
+  }
 }
 
 // ---------------------------------------------------------------------------
