@@ -77,3 +77,38 @@ extern "C" int loom_hip_probe_slice_read(const void* src, uint64_t bytes, uint32
                      static_cast<const u32x4*>(src), bytes / 16 / blocks, sink);
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
+
+// Random-chunk gather: the buffer is `chunks` chunks of `chunk_bytes` (a
+// multiple of 16) and the reads visit them in the order of `perm`, 16 bytes
+// per lane, consecutive lanes on consecutive bytes of a chunk, eight loads per
+// thread in flight. It is the attainable rate of a paged access pattern (K/V
+// blocks scattered by a block table) with no computation.
+__global__ __launch_bounds__(256) void gather_read_kernel(const uint8_t* __restrict__ base,
+                                                          const uint32_t* __restrict__ perm, uint32_t chunks,
+                                                          uint32_t chunk_bytes, uint32_t* __restrict__ sink) {
+  const uint32_t pieces = chunk_bytes / 16;
+  const uint64_t total = static_cast<uint64_t>(chunks) * pieces;
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  u32x4 acc = {0U, 0U, 0U, 0U};
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += 8 * stride) {
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint64_t j = i + k * stride;
+      v[k] = j < total ? *reinterpret_cast<const u32x4*>(base + static_cast<uint64_t>(perm[j / pieces]) * chunk_bytes +
+                                                          (j % pieces) * 16)
+                       : u32x4{0U, 0U, 0U, 0U};
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc ^= v[k];
+  }
+  sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
+extern "C" int loom_hip_probe_gather_read(const void* base, const uint32_t* perm, uint32_t chunks,
+                                          uint32_t chunk_bytes, uint32_t* sink, uint32_t blocks, void* stream) {
+  if (base == nullptr || perm == nullptr || sink == nullptr || chunk_bytes % 16 != 0 || blocks == 0) return 1;
+  hipLaunchKernelGGL(gather_read_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(base), perm, chunks, chunk_bytes, sink);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}

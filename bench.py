@@ -82,6 +82,49 @@ def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
     return moved / sec / 1e9
 
 
+def gather_read_probe(chunk_bytes: int = 16384, nbytes: int = 2 << 30, iters: int = 5,
+                      per_cu=(8, 16)) -> float:
+    """Attainable rate of a paged access pattern: ``nbytes`` read as randomly
+    permuted chunks of ``chunk_bytes`` (a K/V block of C3/C4 is 16-32 KiB),
+    best over grids of ``per_cu`` 256-thread workgroups per CU."""
+    import ctypes
+
+    import torch
+
+    from attnarc_amd import build as _b
+
+    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
+    lib.loom_hip_probe_gather_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                               ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
+    chunks = nbytes // chunk_bytes
+    base = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    perm = torch.randperm(chunks, generator=g, device="cuda").to(torch.int32)
+    props = torch.cuda.get_device_properties(0)
+    sink = torch.empty(props.multi_processor_count * max(per_cu) * 256, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    best = 0.0
+    for k in per_cu:
+        blocks = props.multi_processor_count * k
+
+        def once():
+            assert lib.loom_hip_probe_gather_read(base.data_ptr(), perm.data_ptr(), chunks, chunk_bytes,
+                                                  sink.data_ptr(), blocks, stream) == 0
+
+        once()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            once()
+        b.record()
+        torch.cuda.synchronize()
+        best = max(best, nbytes * iters / (a.elapsed_time(b) * 1e-3) / 1e9)
+    return best
+
+
 def slice_probe(workgroups: int, nbytes: int = 64 << 20, copies: int = 16, iters: int = 20) -> float:
     """Read rate of ``workgroups`` 512-thread workgroups (one per CU), each
     streaming a contiguous slice; ``copies`` rotated buffers keep the reads out
@@ -595,6 +638,8 @@ def main() -> int:
             traffic = t.get("bytes_per_launch")
 
     peak_read = hbm_probe("read")
+    block_bytes = case.block_size * case.kv_heads * case.head_size * case.kv_elem_bytes
+    gather_read = gather_read_probe(block_bytes)
 
     enc = _native.KV_CACHE_FP8_E4M3 if case.cache_encoding == "fp8" else _native.KV_CACHE_NATIVE
     qdt = {torch.float32: _native.F32, torch.float16: _native.F16, torch.bfloat16: _native.BF16}[case.dtype]
@@ -650,6 +695,9 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "measured_stream_read_gbps": round(peak_read, 1),
             "frac_of_measured": round(achieved / peak_read, 4),
+            "measured_block_gather_gbps": round(gather_read, 1),
+            "block_gather_chunk_bytes": block_bytes,
+            "frac_of_block_gather": round(achieved / gather_read, 4),
             "traffic": traffic,
             "kernel": kernel_name,
         },
