@@ -83,7 +83,7 @@ def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
 
 
 def gather_read_probe(chunk_bytes: int = 16384, nbytes: int = 2 << 30, iters: int = 5,
-                      per_cu=(8, 16)) -> float:
+                      per_cu=(2, 4, 8)) -> float:
     """Attainable rate of a paged access pattern: ``nbytes`` read as randomly
     permuted chunks of ``chunk_bytes`` (a K/V block of C3/C4 is 16-32 KiB),
     best over grids of ``per_cu`` 256-thread workgroups per CU."""
