@@ -1,0 +1,27 @@
+"""The per-wave timeline summary (attnarc_amd.wave_trace) on synthetic records (host only)."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from attnarc_amd import wave_trace, workloads
+
+
+def test_summary_of_synthetic_records():
+    case = workloads.make_case(name="trace", dtype=torch.bfloat16, sequences=2, query_heads=8, kv_heads=2,
+                               head_size=64, value_head_size=64, block_size=16, lengths=[1024, 700], seed=1,
+                               device="cpu", pool_factor=1.25, partition_tokens=512)
+    # four waves: three full 512-token partitions and one 188-token partial one
+    rec = np.zeros(4, dtype=wave_trace.RECORD)
+    rec["t0"] = [1000, 1000, 3000, 3500]          # 100 MHz ticks
+    rec["t1"] = [3000, 3500, 5000, 4500]
+    rec["xcc"] = [0, 1, 0, 1]
+    rec["tokens"] = [512, 512, 512, 188]
+    text = wave_trace.summarize(rec, case)
+    assert "first start to last end: 40.0 us" in text
+    row_bytes = 2 * 64 * 2
+    total = (3 * 512 + 188) * row_bytes
+    assert f"KV bytes recorded: {total / 1e9:.4f} GB" in text
+    assert "| 0 | 2 |" in text and "| 1 | 2 |" in text  # two items per XCC
+    assert "| 0-20 | 2 | 22.5 / 20.0 / 25.0 |" in text
