@@ -5,9 +5,10 @@ Counterpart of the reference's ``loom_kernels.torch_ops`` facade
 ops/rope_kv.py, ops/telemetry.py) for the two operators this library
 implements. Loading registers ``torch.ops.loom_kernels.paged_decode_attention``,
 ``torch.ops.loom_kernels.rope_paged_kv_write_`` and the bridge telemetry ops
-from ``attnarc_amd/_build/libloom_hip_torch.so``; every launch runs
-adapter contract check -> bridge checks -> HIP kernels, on torch's current
-stream, with split-K workspaces from the torch caching allocator.
+from ``attnarc_amd/_build/libloom_hip_torch.so``; every launch runs the
+library's tensor-view contract tables -> bridge checks -> HIP kernels, on
+torch's current stream, with split-K workspaces from the torch caching
+allocator.
 
 ``attnarc_amd.ops`` is the ctypes path over the same kernels (and the extended
 decode entry point); this module is the one a torch program or torch.compile
