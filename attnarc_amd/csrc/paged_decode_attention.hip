@@ -3044,11 +3044,22 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxScratchDevices] = {};
 
-int scratch_address(float** out) {
+int scratch_address(hipStream_t stream, float** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) {
     (void)hipGetLastError();
     return fail(LOOM_HIP_UNAVAILABLE, "no current HIP device");
+  }
+  // The array's address is the current device's; the launch stream must be
+  // on that device too.
+  if (stream != nullptr) {
+    hipDevice_t stream_dev = -1;
+    if (hipStreamGetDevice(stream, &stream_dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(LOOM_HIP_INVALID_ARGUMENT, "the stream's device cannot be queried");
+    }
+    if (stream_dev != dev)
+      return fail(LOOM_HIP_INVALID_ARGUMENT, "no-allocation calls need the stream on the current device");
   }
   if (dev < 0 || dev >= kMaxScratchDevices)
     return fail(LOOM_HIP_UNSUPPORTED, "device ordinal beyond the static workspace table");
@@ -3073,7 +3084,7 @@ int run(Problem p, void* stream) {
   if (p.static_workspace) {
     const uint64_t parts = parts_for(p.max_sequence_length, p.partition_tokens);
     if (parts > 1) {
-      status = scratch_address(&p.workspace);
+      status = scratch_address(static_cast<hipStream_t>(stream), &p.workspace);
       if (status != LOOM_HIP_SUCCESS) return status;
       p.workspace_elements = LOOM_HIP_STATIC_WORKSPACE_ELEMENTS;
     }

@@ -241,9 +241,11 @@ int loom_hip_paged_decode_attention_extended_bf16(
  * holds on each device it runs on until the process ends. A call whose
  * states need more (the extended sizing function's count) returns
  * LOOM_HIP_UNSUPPORTED before launching anything. Nothing is allocated,
- * freed or cleared by the call. All calls on one device share that device's
- * array: calls that may overlap in time on one device (different streams,
- * or different threads without ordering) race and must not be issued.
+ * freed or cleared by the call. The array used is the current device's, so
+ * `stream` must belong to the current device (LOOM_HIP_INVALID_ARGUMENT
+ * otherwise). All calls on one device share that device's array: calls that
+ * may overlap in time on one device (different streams, or different threads
+ * without ordering) race and must not be issued.
  */
 #define LOOM_HIP_STATIC_WORKSPACE_ELEMENTS (16ULL * 1024ULL * 1024ULL)
 
