@@ -4,7 +4,6 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-#include <stdint.h>
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
