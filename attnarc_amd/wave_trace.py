@@ -67,12 +67,21 @@ def summarize(rec: np.ndarray, case) -> str:
     end = (rec["t1"] - t0) / 100.0
     dur = end - start
     row_bytes = (case.head_size + case.value_head_size) * case.kv_elem_bytes
-    nbytes = rec["tokens"].astype(np.float64) * row_bytes
+    # Waves that split one item (the 4-wave split of small grids) each record
+    # the whole item: share its bytes among them.
+    key = (rec["seq"].astype(np.uint64) << np.uint64(40)) | (rec["part"].astype(np.uint64) << np.uint64(20)) \
+        | rec["kvh"].astype(np.uint64)
+    _, inverse, counts = np.unique(key, return_inverse=True, return_counts=True)
+    nbytes = rec["tokens"].astype(np.float64) * row_bytes / counts[inverse]
     full = rec["tokens"] == case.partition_tokens
     lines = [f"# Wave timeline: {case.name}", "",
              f"- waves with work: {len(rec)}; first start to last end: {end.max():.1f} us",
              f"- KV bytes recorded: {nbytes.sum() / 1e9:.4f} GB (the call's algorithmic bytes: {case.kv_bytes() / 1e9:.4f} GB)",
-             f"- whole-launch rate: {nbytes.sum() / end.max() / 1e3:.0f} GB/s", "",
+             f"- whole-launch rate: {nbytes.sum() / end.max() / 1e3:.0f} GB/s",
+             "- wave start times, percentiles 10 / 50 / 90 / 100: "
+             + " / ".join(f"{np.percentile(start, q):.1f}" for q in (10, 50, 90, 100)) + " us",
+             "- wave end times, percentiles 0 / 10 / 50 / 90: "
+             + " / ".join(f"{np.percentile(end, q):.1f}" for q in (0, 10, 50, 90)) + " us", "",
              "## Over time (10 us windows)", "",
              "| window (us) | waves running | items started (full / partial) | KV GB/s, items spread evenly |",
              "|---|---|---|---|"]
