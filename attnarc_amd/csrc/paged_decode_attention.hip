@@ -40,6 +40,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <limits>
@@ -2404,6 +2405,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
 // ---------------------------------------------------------------------------
 thread_local std::string g_last_error;
 thread_local const char* g_last_family = "";
+thread_local uint32_t g_last_internal_split = 0;
 std::atomic<uint64_t> g_decode_launches{0};
 std::atomic<uint64_t> g_rope_launches{0};
 
@@ -3076,6 +3078,105 @@ int scratch_address(hipStream_t stream, float** out) {
   return LOOM_HIP_SUCCESS;
 }
 
+// Internal split of single-partition calls. A call whose (sequence, KV head)
+// items cannot fill the CUs (C2's 64 items put 4 waves on each of 64 of the
+// 256 CUs, and 64 CUs pull at most ~3.1 TB/s) is run as a split-K call with
+// partial states in a library-held slot, then merged into the caller's
+// output: the caller still passes no workspace. The slots are one static
+// array per device, kPoolSlots slots of kPoolSlotElements F32 elements
+// (32 MiB per device, resident until the process ends). The first
+// kPoolSlots streams that make such a call on a device each own one slot
+// until the process ends; calls on one stream use its slot in stream order,
+// so no call waits for another and no event is recorded (an event record
+// after every call measured 3 us per call on C2, 1 us without its system
+// fence). A stream handle names a live stream object: a handle can only come
+// back after its stream was destroyed and its work drained, so a reused
+// handle inherits an idle slot. Calls from further streams, from
+// hipStreamPerThread (one handle for many streams), under stream capture (a
+// graph would keep the slot's address), or made while the environment
+// variable LOOM_HIP_INTERNAL_SPLIT is "0" run as one partition per item.
+constexpr int kPoolSlots = 8;
+constexpr uint64_t kPoolSlotElements = 1024ULL * 1024ULL;
+__device__ __align__(256) float split_pool[kPoolSlots * kPoolSlotElements];
+
+struct DevicePool {
+  float* base = nullptr;
+  bool unavailable = false;
+  int owners = 0;
+  hipStream_t owner[kPoolSlots] = {};
+};
+
+std::mutex g_pool_mu;
+DevicePool g_pool[kMaxScratchDevices];
+
+// Partition size of the internal split, or 0 when the call stays whole:
+// fewer items than CUs, at least 1024 tokens, partitions of 128 tokens or
+// more sized so that the grid stays within about 2048 items, at most 256
+// partitions per sequence, and states that fit one slot.
+uint32_t internal_partition_tokens(const Problem& p) {
+  const uint64_t items = static_cast<uint64_t>(p.sequences) * p.kv_heads;
+  if (items >= 256 || p.max_sequence_length < 1024) return 0;
+  const uint64_t len = p.max_sequence_length;
+  const uint64_t row = static_cast<uint64_t>(p.sequences) * p.query_heads * (p.value_head_size + 2ULL);
+  uint64_t t = 128;
+  while (t < len && (items * ((len + t - 1) / t) > 2048 || (len + t - 1) / t > 256 ||
+                     row * ((len + t - 1) / t) > kPoolSlotElements))
+    t *= 2;
+  const uint64_t parts = (len + t - 1) / t;
+  if (parts < 2 || row * parts > kPoolSlotElements) return 0;
+  return static_cast<uint32_t>(t);
+}
+
+bool internal_split_enabled() {
+  const char* v = getenv("LOOM_HIP_INTERNAL_SPLIT");
+  return v == nullptr || strcmp(v, "0") != 0;
+}
+
+// The slot of `stream` on the current device, claiming a free one on the
+// stream's first call; nullptr when the call runs as one partition.
+float* stream_slot(hipStream_t stream) {
+  if (stream == hipStreamPerThread) return nullptr;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (capture != hipStreamCaptureStatusNone) return nullptr;
+  if (stream != nullptr && stream != hipStreamLegacy) {
+    hipDevice_t stream_dev = -1;
+    if (hipStreamGetDevice(stream, &stream_dev) != hipSuccess || stream_dev != dev) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
+  std::lock_guard<std::mutex> lock(g_pool_mu);
+  DevicePool& pool = g_pool[dev];
+  if (pool.unavailable) return nullptr;
+  if (pool.base == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(split_pool)) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      pool.unavailable = true;
+      return nullptr;
+    }
+    pool.base = static_cast<float*>(ptr);
+  }
+  int pick = -1;
+  for (int i = 0; i < pool.owners && pick < 0; ++i)
+    if (pool.owner[i] == stream) pick = i;
+  if (pick < 0) {
+    if (pool.owners == kPoolSlots) return nullptr;
+    pick = pool.owners++;
+    pool.owner[pick] = stream;
+  }
+  return pool.base + static_cast<uint64_t>(pick) * kPoolSlotElements;
+}
+
 int run(Problem p, void* stream) {
   int status = validate(p);
   if (status != LOOM_HIP_SUCCESS) return status;
@@ -3090,12 +3191,26 @@ int run(Problem p, void* stream) {
     }
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t internal = 0;
+  if (!p.static_workspace && parts_for(p.max_sequence_length, p.partition_tokens) == 1) {
+    const uint32_t t = internal_partition_tokens(p);
+    float* slot = t != 0 && internal_split_enabled() ? stream_slot(s) : nullptr;
+    if (slot != nullptr) {
+      p.partition_tokens = t;
+      p.workspace = slot;
+      p.workspace_elements = kPoolSlotElements;
+      internal = t;
+    }
+  }
   switch (p.dtype) {
     case kF32: status = run_typed<F32Elem>(p, s); break;
     case kF16: status = run_typed<F16Elem>(p, s); break;
     default: status = run_typed<Bf16Elem>(p, s); break;
   }
-  if (status == LOOM_HIP_SUCCESS) g_decode_launches.fetch_add(1, std::memory_order_relaxed);
+  if (status == LOOM_HIP_SUCCESS) {
+    g_last_internal_split = internal;
+    g_decode_launches.fetch_add(1, std::memory_order_relaxed);
+  }
   return status;
 }
 
@@ -3282,6 +3397,8 @@ uint32_t loom_hip_abi_version(void) { return 1; }
 const char* loom_hip_last_error_message(void) { return g_last_error.c_str(); }
 
 const char* loom_hip_last_kernel_family(void) { return g_last_family; }
+
+uint32_t loom_hip_last_internal_partition_tokens(void) { return g_last_internal_split; }
 
 int loom_hip_launch_count(uint32_t operation, uint64_t* count) {
   if ((operation != LOOM_HIP_PAGED_DECODE_ATTENTION && operation != LOOM_HIP_ROPE_PAGED_KV_WRITE) ||

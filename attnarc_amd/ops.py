@@ -456,6 +456,12 @@ def last_kernel_family() -> str:
     return _native.lib().loom_hip_last_kernel_family().decode()
 
 
+def last_internal_partition_tokens() -> int:
+    """Partition size of the internal split of the last successful paged-decode
+    call on this thread (0: it ran as the caller asked)."""
+    return int(_native.lib().loom_hip_last_internal_partition_tokens())
+
+
 def launch_count(operation: int = _native.PAGED_DECODE_ATTENTION) -> int:
     count = ctypes.c_uint64()
     _native.check(_native.lib().loom_hip_launch_count(operation, ctypes.byref(count)), "launch count")

@@ -597,6 +597,9 @@ def main() -> int:
     dec_ms, dec_n = ops.kernel_timing_read(_native.KERNEL_DECODE)
     mrg_ms, mrg_n = ops.kernel_timing_read(_native.KERNEL_MERGE)
     ops.kernel_timing_enable(False)
+    # A single-partition call on a small grid is split inside the library
+    # (eager calls only; a captured call keeps one partition).
+    internal_pt = ops.last_internal_partition_tokens()
     dec_us = dec_ms / max(dec_n, 1) * 1e3
     mrg_us = mrg_ms / max(mrg_n, 1) * 1e3 if mrg_n else 0.0
     achieved = kv_bytes / (dec_us * 1e-6) / 1e9
@@ -654,7 +657,7 @@ def main() -> int:
         # the library's launch rule: grouped single-wave items for >= 4096 work items, or >= 1024
         # with partitions of 8+ steps of 16 tokens (head size 256: >= 4096 only); none for groups
         # of more than 16 query heads
-        pt = case.partition_tokens or case.max_sequence_length
+        pt = internal_pt or case.partition_tokens or case.max_sequence_length
         items = -(-case.max_sequence_length // pt) * case.kv_heads * case.sequences
         steps = -(-pt // 16)
         grouped = items >= 4096 or (items >= 1024 and steps >= 8 and case.head_size != 256)
@@ -686,7 +689,7 @@ def main() -> int:
         "dtype": "bf16" if case.dtype == torch.bfloat16 else str(case.dtype).replace("torch.", ""),
         "data": "synthetic (seeded N(0,1) Q/K/V rounded to the storage dtype, seeded lengths and shuffled block table)",
         "config": {**case.describe(), "kv_bytes_per_call": kv_bytes, "kv_pool_copies_rotated": copies,
-                   "parallelism": "none (1 GPU)"},
+                   "internal_partition_tokens": internal_pt, "parallelism": "none (1 GPU)"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),

@@ -80,8 +80,10 @@ const char* loom_hip_status_string(int status);
  * K/V caches have dense inner NHD [block_size, kv_heads, dim] dimensions and
  * an explicit element stride between blocks (separate caches or vLLM's
  * interleaved [blocks, 2, block_size, kv_heads, dim] storage). F16/BF16 data
- * is passed as uint16_t bit patterns. No workspace: each (sequence, KV head)
- * is reduced inside one workgroup.
+ * is passed as uint16_t bit patterns. No caller workspace: a (sequence, KV
+ * head) is reduced inside one workgroup, except for small grids with long
+ * contexts, which the library splits over a slot of its own (see
+ * loom_hip_last_internal_partition_tokens).
  */
 int loom_hip_paged_decode_attention_f32(
     const float* query, const float* key_cache, const float* value_cache,
@@ -368,6 +370,21 @@ const char* loom_hip_last_error_message(void);
  * capability query does not see.
  */
 const char* loom_hip_last_kernel_family(void);
+
+/*
+ * Partition size (tokens) of the internal split that the last successful
+ * paged decode call on this thread ran, or 0 when it ran as the caller asked.
+ * Single-partition calls (no caller workspace) whose (sequence, KV head)
+ * items cannot fill the GPU and whose context reaches 1024 tokens are split
+ * with their partial states in a library-held slot: a static array per
+ * device of 8 slots x 4 MiB, resident until the process ends. The first 8
+ * streams that make such a call on a device each keep one slot (calls on one
+ * stream use it in stream order). Calls from other streams, from
+ * hipStreamPerThread, under stream capture, and all calls while the
+ * environment variable LOOM_HIP_INTERNAL_SPLIT is "0" run as one partition.
+ * No reference counterpart: a diagnostic.
+ */
+uint32_t loom_hip_last_internal_partition_tokens(void);
 
 /*
  * Relaxed atomic launch counters (replace loom_cuda_bridge_launch_count /
