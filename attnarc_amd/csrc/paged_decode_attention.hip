@@ -3084,7 +3084,7 @@ int scratch_address(hipStream_t stream, float** out) {
 // partial states in a library-held slot, then merged into the caller's
 // output: the caller still passes no workspace. The slots are one static
 // array per device, kPoolSlots slots of kPoolSlotElements F32 elements
-// (32 MiB per device, resident until the process ends). The first
+// (64 MiB per device, resident until the process ends). The first
 // kPoolSlots streams that make such a call on a device each own one slot
 // until the process ends; calls on one stream use its slot in stream order,
 // so no call waits for another and no event is recorded (an event record
@@ -3095,8 +3095,8 @@ int scratch_address(hipStream_t stream, float** out) {
 // hipStreamPerThread (one handle for many streams), under stream capture (a
 // graph would keep the slot's address), or made while the environment
 // variable LOOM_HIP_INTERNAL_SPLIT is "0" run as one partition per item.
-constexpr int kPoolSlots = 8;
-constexpr uint64_t kPoolSlotElements = 1024ULL * 1024ULL;
+constexpr int kPoolSlots = 4;
+constexpr uint64_t kPoolSlotElements = 4ULL * 1024ULL * 1024ULL;
 __device__ __align__(256) float split_pool[kPoolSlots * kPoolSlotElements];
 
 struct DevicePool {
@@ -3110,12 +3110,16 @@ std::mutex g_pool_mu;
 DevicePool g_pool[kMaxScratchDevices];
 
 // Partition size of the internal split, or 0 when the call stays whole:
-// fewer items than CUs, at least 1024 tokens, partitions of 128 tokens or
+// fewer items than CUs, at least 2048 tokens, partitions of 128 tokens or
 // more sized so that the grid stays within about 2048 items, at most 256
-// partitions per sequence, and states that fit one slot.
+// partitions per sequence, and states that fit one slot. Measured as whole
+// calls (us, one partition against the split): 16 items x 1024 tokens 15.2
+// against 17.0 (the merge launch costs more than the split gains), C2's 64 x
+// 2048 28.2 against 20.4, 64 x 8192 99.6 against 53.5, 4 MQA items x 32768
+// 1423 against 28.8; 256 items x 4096 96.7 against 98.5-108 (no gain).
 uint32_t internal_partition_tokens(const Problem& p) {
   const uint64_t items = static_cast<uint64_t>(p.sequences) * p.kv_heads;
-  if (items >= 256 || p.max_sequence_length < 1024) return 0;
+  if (items >= 256 || p.max_sequence_length < 2048) return 0;
   const uint64_t len = p.max_sequence_length;
   const uint64_t row = static_cast<uint64_t>(p.sequences) * p.query_heads * (p.value_head_size + 2ULL);
   uint64_t t = 128;

@@ -375,9 +375,9 @@ const char* loom_hip_last_kernel_family(void);
  * Partition size (tokens) of the internal split that the last successful
  * paged decode call on this thread ran, or 0 when it ran as the caller asked.
  * Single-partition calls (no caller workspace) whose (sequence, KV head)
- * items cannot fill the GPU and whose context reaches 1024 tokens are split
+ * items cannot fill the GPU and whose context reaches 2048 tokens are split
  * with their partial states in a library-held slot: a static array per
- * device of 8 slots x 4 MiB, resident until the process ends. The first 8
+ * device of 4 slots x 16 MiB, resident until the process ends. The first 4
  * streams that make such a call on a device each keep one slot (calls on one
  * stream use it in stream order). Calls from other streams, from
  * hipStreamPerThread, under stream capture, and all calls while the

@@ -1,9 +1,9 @@
 """Single-partition calls that the library splits internally (run on an MI355X).
 
 A call with no caller workspace whose (sequence, KV head) items cannot fill
-the CUs and whose context reaches 1024 tokens runs as a split-K call with its
+the CUs and whose context reaches 2048 tokens runs as a split-K call with its
 partial states in a library-held slot (one static array per device, one slot
-for each of the first eight streams), then merges into the caller's output. These tests check the
+for each of the first four streams), then merges into the caller's output. These tests check the
 results against the oracle, that the split really ran (a merge launch), that
 LOOM_HIP_INTERNAL_SPLIT=0 keeps one partition, that calls on more streams than
 there are slots stay correct when they overlap, and that a call under stream
@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from attnarc_amd import _native, ops, workloads
-from gpu_util import LSE_TOL, assert_parity, oracle_expected
+from gpu_util import LSE_TOL, ORACLE_THREADS, assert_parity, oracle_expected
 
 pytestmark = pytest.mark.gpu
 
@@ -103,7 +103,7 @@ def test_environment_switch_keeps_one_partition(no_internal_split):
 
 
 def test_large_grid_or_short_context_stays_whole():
-    short = _case(14, lengths=(1000, 700, 999, 512))
+    short = _case(14, lengths=(2047, 700, 999, 512))  # contexts under 2048 stay whole
     _, merges = _merges(lambda: workloads.run_case(short))
     assert merges == 0 and ops.last_internal_partition_tokens() == 0
     wide = _case(15, lengths=[1024] * 32, hq=64, hkv=8)  # 256 items
@@ -112,7 +112,7 @@ def test_large_grid_or_short_context_stays_whole():
 
 
 def test_overlapping_calls_on_more_streams_than_slots():
-    """Ten streams (the pool has eight slots per device, so some streams run
+    """Ten streams (the pool has four slots per device, so some streams run
     whole), each call enqueued behind a long kernel on its stream so that the
     calls overlap; every stream runs two calls with different inputs, then
     all results are checked."""
@@ -157,3 +157,14 @@ def test_call_under_stream_capture_keeps_one_partition_and_replays():
         assert_parity(out, expected, torch.bfloat16, f"graph replay {i}")
         workloads.run_case(case)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_long_mqa_single_partition_splits_internally():
+    """Four MQA items (32 query heads on one KV head) of up to 32768 tokens:
+    as one partition each, 4 of the 256 CUs would work."""
+    case = _case(17, lengths=(32768, 30001, 16384, 20480), hq=32, hkv=1)
+    (out, lse), merges = _merges(lambda: workloads.run_case(case, return_lse=True))
+    assert merges == 1 and ops.last_internal_partition_tokens() == 256
+    expected, want_lse = oracle_expected(case, threads=ORACLE_THREADS)
+    assert_parity(out, expected, torch.bfloat16, "long MQA, internal split")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
