@@ -3109,23 +3109,25 @@ struct DevicePool {
 std::mutex g_pool_mu;
 DevicePool g_pool[kMaxScratchDevices];
 
-// Partition size of the internal split, or 0 when the call stays whole:
-// fewer items than CUs, at least 2048 tokens, partitions of 128 tokens or
-// more sized so that the grid stays within about 2048 items, at most 256
-// partitions per sequence, and states that fit one slot. Measured as whole
-// calls (us, one partition against the split): 16 items x 1024 tokens 15.2
-// against 17.0 (the merge launch costs more than the split gains), C2's 64 x
-// 2048 28.2 against 20.4, 64 x 8192 99.6 against 53.5, 4 MQA items x 32768
-// 1423 against 28.8; 256 items x 4096 96.7 against 98.5-108 (no gain).
+uint32_t split_k_partition_tokens(uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+                                  uint32_t head_size, uint32_t value_head_size,
+                                  uint32_t max_sequence_length);
+
+// Partition size of the internal split, or 0 when the call stays whole: the
+// split entry points' policy (fewer items than CUs) for contexts of at least
+// 2048 tokens, with partitions doubled until a sequence has at most 256 and
+// the states fit one slot. Measured as whole calls (us, one partition against
+// the split): 16 items x 1024 tokens 15.2 against 17.0 (the merge launch
+// costs more than the split gains), C2's 64 x 2048 28.2 against 20.4,
+// 64 x 8192 99.6 against 53.7, 4 MQA items x 32768 1423 against 30.0.
 uint32_t internal_partition_tokens(const Problem& p) {
-  const uint64_t items = static_cast<uint64_t>(p.sequences) * p.kv_heads;
-  if (items >= 256 || p.max_sequence_length < 2048) return 0;
+  if (p.max_sequence_length < 2048) return 0;
+  uint64_t t = split_k_partition_tokens(p.sequences, p.query_heads, p.kv_heads, p.head_size, p.value_head_size,
+                                        p.max_sequence_length);
+  if (t == 0) return 0;
   const uint64_t len = p.max_sequence_length;
   const uint64_t row = static_cast<uint64_t>(p.sequences) * p.query_heads * (p.value_head_size + 2ULL);
-  uint64_t t = 128;
-  while (t < len && (items * ((len + t - 1) / t) > 2048 || (len + t - 1) / t > 256 ||
-                     row * ((len + t - 1) / t) > kPoolSlotElements))
-    t *= 2;
+  while (t < len && ((len + t - 1) / t > 256 || row * ((len + t - 1) / t) > kPoolSlotElements)) t *= 2;
   const uint64_t parts = (len + t - 1) / t;
   if (parts < 2 || row * parts > kPoolSlotElements) return 0;
   return static_cast<uint32_t>(t);
@@ -3219,9 +3221,12 @@ int run(Problem p, void* stream) {
 }
 
 // Split-K policy of the reference-compatible split entry points. The shape
-// splits when (sequence, KV head) work items alone cannot fill the 256 CUs
-// and the context is long enough: partitions of at least 512 tokens, sized
-// so that the grid reaches about 2048 workgroups.
+// splits when there are fewer (sequence, KV head) work items than the 256
+// CUs and the context reaches 512 tokens: partitions of at least 64 tokens
+// (a multiple of 32), sized so that the grid reaches about 1024 items.
+// Measured as whole calls (us, by partition size): 64 items x 2048 tokens
+// 64: 22.3, 128: 20.4, 256: 21.4; 64 x 8192 256: 55.1, 512: 53.7; from 256
+// items (x 2048-4096 tokens) every split measured 1-3% slower than none.
 uint32_t split_k_partition_tokens(uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
                                   uint32_t head_size, uint32_t value_head_size,
                                   uint32_t max_sequence_length) {
@@ -3229,12 +3234,11 @@ uint32_t split_k_partition_tokens(uint32_t sequences, uint32_t query_heads, uint
       value_head_size == 0 || max_sequence_length == 0 || query_heads % kv_heads != 0)
     return 0;
   const uint64_t work = static_cast<uint64_t>(sequences) * kv_heads;
-  if (work >= 1024 || max_sequence_length < 512) return 0;
-  const uint64_t want_parts = (2048 + work - 1) / work;
+  if (work >= 256 || max_sequence_length < 512) return 0;
+  const uint64_t want_parts = (1024 + work - 1) / work;
   uint64_t tokens = (max_sequence_length + want_parts - 1) / want_parts;
   tokens = ((tokens + kChunk - 1) / kChunk) * kChunk;
-  const uint64_t floor_tokens = work < 256 ? 64 : 512;
-  if (tokens < floor_tokens) tokens = floor_tokens;
+  if (tokens < 64) tokens = 64;
   if (parts_for(max_sequence_length, static_cast<uint32_t>(tokens)) < 2) return 0;
   return static_cast<uint32_t>(tokens);
 }

@@ -103,14 +103,16 @@ def test_split_k_sizing_policy():
     ws = lib.loom_hip_paged_decode_attention_split_k_workspace_elements
     # plenty of (sequence, kv head) work or a short context: base path
     assert ws(256, 32, 8, 128, 128, 8192) == 0
-    assert ws(64, 32, 8, 128, 128, 8192) == 64 * 32 * 4 * 130  # 512 work items: 4 parts of 2048
+    assert ws(32, 32, 8, 128, 128, 8192) == 0  # 256 work items fill the CUs
+    assert ws(16, 32, 8, 128, 128, 4096) == 16 * 32 * 8 * 130  # 128 work items: 8 parts of 512
+    assert ws(32, 12, 2, 128, 128, 2048) == 32 * 12 * 16 * 130  # C2: 64 work items, 16 parts of 128
     assert ws(8, 32, 8, 128, 128, 511) == 0
     # fewer work items than CUs: 64-token partitions from a 512-token context on
     assert ws(8, 32, 8, 128, 128, 512) == 8 * 32 * 8 * 130
     assert ws(8, 32, 8, 128, 128, 1024) == 8 * 32 * 16 * 130
-    # a grid that already covers the CUs keeps 512-token partitions
+    # a grid that already covers the CUs stays whole
     assert ws(32, 32, 8, 128, 128, 512) == 0
-    assert ws(32, 32, 8, 128, 128, 1024) == 32 * 32 * 2 * 130
+    assert ws(32, 32, 8, 128, 128, 1024) == 0
     assert ws(0, 32, 8, 128, 128, 4096) == 0
     assert ws(8, 30, 8, 128, 128, 4096) == 0  # heads not divisible
     # long context, small grid: split; size = B*Hq*parts*(Dv+2)

@@ -63,7 +63,7 @@ def test_small_grid_long_context_splits_internally(dtype, encoding, layout):
     case = _case(11, dtype=dtype, encoding=encoding, layout=layout)
     (out, lse), merges = _merges(lambda: workloads.run_case(case, return_lse=True))
     assert merges == 1, "a single-partition call of 8 items and 2048 tokens should split internally"
-    assert ops.last_internal_partition_tokens() == 128  # 16 partitions x 8 items
+    assert ops.last_internal_partition_tokens() == 64  # 32 partitions x 8 items
     expected, want_lse = oracle_expected(case)
     assert_parity(out, expected, dtype, f"internal split {dtype} {encoding} {layout}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
@@ -88,7 +88,7 @@ def test_base_entry_point_splits_internally():
         return out
 
     _, merges = _merges(call)
-    assert merges == 1 and ops.last_internal_partition_tokens() == 128
+    assert merges == 1 and ops.last_internal_partition_tokens() == 64
     expected, _ = oracle_expected(case)
     assert_parity(out, expected, torch.bfloat16, "base entry, internal split")
 
