@@ -1585,6 +1585,37 @@ struct WaveStamp {
   }
 };
 #define LOOM_WAVE_STAMP(slot) WaveStamp wave_stamp{(slot), __builtin_amdgcn_s_memrealtime()}
+// Times at which a wave starts its step loop (its Q and first steps' K/V have
+// arrived) and reaches 1/4, 1/2 and 3/4 of its steps (record of the same
+// wave slot; the slot is the wave's index in the launch).
+__device__ unsigned long long g_wave_marks[kWaveRecords][4];
+// Time a wave spends waiting for its step loads, per quarter of its steps.
+__device__ unsigned long long g_wave_stall[kWaveRecords][4];
+#define LOOM_WAVE_STALL_DECL unsigned long long wave_stall[4] = {0ULL, 0ULL, 0ULL, 0ULL}
+#define LOOM_WAVE_STALL(step, total, wait_stmt)                                               \
+  do {                                                                                        \
+    const unsigned long long w0 = __builtin_amdgcn_s_memrealtime();                          \
+    wait_stmt;                                                                                \
+    const unsigned long long w1 = __builtin_amdgcn_s_memrealtime();                          \
+    const uint32_t quarter = min(4U * (step) / max((total), 1U), 3U);                        \
+    _Pragma("unroll") for (uint32_t q = 0; q < 4; ++q) if (q == quarter) wave_stall[q] += w1 - w0; \
+  } while (0)
+#define LOOM_WAVE_STALL_STORE                                                                 \
+  do {                                                                                        \
+    const uint32_t wave_slot = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);          \
+    if ((threadIdx.x & 63U) == 0 && wave_slot < kWaveRecords)                                 \
+      _Pragma("unroll") for (uint32_t q = 0; q < 4; ++q) g_wave_stall[wave_slot][q] = wave_stall[q]; \
+  } while (0)
+#define LOOM_WAVE_MARK(n, stride, total)                                                      \
+  do {                                                                                        \
+    const uint32_t wave_slot = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);          \
+    _Pragma("unroll") for (uint32_t q = 0; q < 4; ++q) {                                      \
+      const uint32_t target = q * (total) / 4U;                                               \
+      if (target >= (n) && target < (n) + (stride) && (threadIdx.x & 63U) == 0 &&             \
+          wave_slot < kWaveRecords)                                                           \
+        g_wave_marks[wave_slot][q] = __builtin_amdgcn_s_memrealtime();                       \
+    }                                                                                         \
+  } while (0)
 #define LOOM_WAVE_ITEM(a, item)                                                                            \
   do {                                                                                                     \
     wave_stamp.seq = (item).seq;                                                                           \
@@ -1598,6 +1629,16 @@ struct WaveStamp {
   } while (0)
 #define LOOM_WAVE_ITEM(a, item) \
   do {                          \
+  } while (0)
+#define LOOM_WAVE_MARK(n, stride, total) \
+  do {                                   \
+  } while (0)
+#define LOOM_WAVE_STALL_DECL \
+  do {                       \
+  } while (0)
+#define LOOM_WAVE_STALL(step, total, wait_stmt) wait_stmt
+#define LOOM_WAVE_STALL_STORE \
+  do {                        \
   } while (0)
 #endif
 
@@ -1827,14 +1868,17 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
         }
       }
     }
+    LOOM_WAVE_STALL_DECL;
     for (uint32_t n = 0; n < my_n; n += S) {
+      LOOM_WAVE_MARK(n, S, my_n);
 #pragma unroll
       for (int i = 0; i < S; ++i) {
         if (n + i < my_n) {
           const uint32_t t0 = t_first + (n + i) * st;
           const uint32_t tn = min(t0 + S * st, t_last);
           uint8_t* vtile = kFp8 ? tw + Dec::kVTileOff : tl[i] + Dec::kVOff;
-          vm_wait_dma<Dec::kDmaPerStep * (S - 1)>();  // this step's loads; S - 1 steps stay in flight
+          // this step's loads; S - 1 steps stay in flight
+          LOOM_WAVE_STALL(n + i, my_n, (vm_wait_dma<Dec::kDmaPerStep * (S - 1)>()));
           scalar_ready(nx[i]);
           if (kFp8) {
             dec.stage_v_fp8(tl[i], vtile, t0);
@@ -1853,6 +1897,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    LOOM_WAVE_STALL_STORE;
   }
 
   float lt[kHT];
@@ -3728,5 +3773,19 @@ extern "C" int loom_hip_wave_trace_read(void* host, uint64_t bytes) {
     if (hipMemcpyToSymbol(HIP_SYMBOL(g_wave_records), zero, sizeof(zero), off, hipMemcpyHostToDevice) != hipSuccess)
       return 1;
   return 0;
+}
+
+// The loop-start and quarter marks of the same wave slots (four u64 per slot); not cleared
+// (every traced wave with steps overwrites its own).
+extern "C" int loom_hip_wave_trace_marks_read(void* host, uint64_t bytes) {
+  const uint64_t n = bytes < sizeof(g_wave_marks) ? bytes : sizeof(g_wave_marks);
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_wave_marks), n, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
+}
+
+// Per quarter of its steps, the time each wave slot spent waiting for step
+// loads (four u64 per slot, 100 MHz ticks); not cleared either.
+extern "C" int loom_hip_wave_trace_stall_read(void* host, uint64_t bytes) {
+  const uint64_t n = bytes < sizeof(g_wave_stall) ? bytes : sizeof(g_wave_stall);
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_wave_stall), n, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
 }
 #endif

@@ -14,7 +14,7 @@ chip over time:
 * per XCC: items, bytes and the time of its last item;
 * the spread of full-item durations among the items that ran on one CU.
 
-Usage: ``python -m attnarc_amd.wave_trace --config 3 [--out FILE]``.
+Usage: ``python -m attnarc_amd.wave_trace --config 3 [--shape SPEC] [--out FILE]``.
 """
 
 from __future__ import annotations
@@ -29,9 +29,15 @@ import numpy as np
 RECORD = np.dtype([("t0", "<u8"), ("t1", "<u8"), ("xcc", "<u4"), ("hw_id", "<u4"), ("seq", "<u4"),
                    ("part", "<u4"), ("kvh", "<u4"), ("tokens", "<u4")])
 RECORDS = 1 << 16
+# A record with the times at which the wave started its step loop (Q and the
+# first steps' K/V arrived) and reached 1/4, 1/2 and 3/4 of its steps.
+# ``stall``: per quarter of the steps, the time spent waiting for step loads.
+RECORD_MARKED = np.dtype(RECORD.descr + [("marks", "<u8", (4,)), ("stall", "<u8", (4,))])
 
 
-def collect(config: int, warmup: int = 5) -> tuple[np.ndarray, object]:
+def collect(config: int, warmup: int = 5, shape: str | None = None, prepare=None) -> tuple[np.ndarray, object]:
+    """Records of one call of configuration ``config`` (or of ``shape``, a
+    workloads.shape_case spec); ``prepare(case)`` may edit the case first."""
     from . import build as _build
 
     if not os.path.exists(_build.WAVE_TRACE_LIB_PATH):
@@ -41,7 +47,9 @@ def collect(config: int, warmup: int = 5) -> tuple[np.ndarray, object]:
 
     from . import _native, workloads
 
-    case = workloads.config(config, "cuda:0")
+    case = workloads.shape_case(shape, "cuda:0") if shape else workloads.config(config, "cuda:0")
+    if prepare is not None:
+        prepare(case)
     lib = _native.lib()
     if os.path.realpath(_native.LIB_PATH) != os.path.realpath(_build.WAVE_TRACE_LIB_PATH):
         raise RuntimeError("the regular library was loaded before wave_trace selected the profiling build")
@@ -58,7 +66,25 @@ def collect(config: int, warmup: int = 5) -> tuple[np.ndarray, object]:
     torch.cuda.synchronize()
     if read(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("wave trace read failed")
-    return buf[buf["tokens"] > 0], case
+    marks_read = lib.loom_hip_wave_trace_marks_read
+    marks_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
+    marks_read.restype = ctypes.c_int
+    marks = np.zeros((RECORDS, 4), dtype="<u8")
+    if marks_read(marks.ctypes.data, marks.nbytes) != 0:
+        raise RuntimeError("wave trace marks read failed")
+    stall_read = lib.loom_hip_wave_trace_stall_read
+    stall_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
+    stall_read.restype = ctypes.c_int
+    stall = np.zeros((RECORDS, 4), dtype="<u8")
+    if stall_read(stall.ctypes.data, stall.nbytes) != 0:
+        raise RuntimeError("wave trace stall read failed")
+    live = buf["tokens"] > 0
+    rec = np.zeros(int(live.sum()), dtype=RECORD_MARKED)
+    for name in RECORD.names:
+        rec[name] = buf[name][live]
+    rec["marks"] = marks[live]
+    rec["stall"] = stall[live]
+    return rec, case
 
 
 def summarize(rec: np.ndarray, case) -> str:
@@ -92,13 +118,42 @@ def summarize(rec: np.ndarray, case) -> str:
         started = (start >= lo) & (start < hi)
         lines.append(f"| {lo:.0f}-{hi:.0f} | {int(((start < hi) & (end > lo)).sum())} | "
                      f"{int((started & full).sum())} / {int((started & ~full).sum())} | {rate:.0f} |")
+    if "marks" in rec.dtype.names:
+        # Each wave's bytes split evenly over its four quarters of steps: the
+        # rate follows each wave's own progress instead of its lifetime.
+        marks = (rec["marks"][:, 1:].astype(np.float64) - t0) / 100.0
+        loop0 = (rec["marks"][:, 0].astype(np.float64) - t0) / 100.0
+        edges = np.column_stack([start, marks, end])
+        lines += ["", "## Over time, from the quarter marks (10 us windows)", "",
+                  "| window (us) | KV GB/s, each quarter of a wave's steps spread over its own time |", "|---|---|"]
+        for lo in np.arange(0, end.max(), 10.0):
+            hi = lo + 10.0
+            total = 0.0
+            for q in range(4):
+                a, b = edges[:, q], edges[:, q + 1]
+                overlap = np.clip(np.minimum(b, hi) - np.maximum(a, lo), 0, None)
+                total += (nbytes / 4 * overlap / np.maximum(b - a, 1e-9)).sum()
+            lines.append(f"| {lo:.0f}-{hi:.0f} | {total / 10e-6 / 1e9:.0f} |")
+    has_marks = "marks" in rec.dtype.names
     lines += ["", "## Full-partition items by start time", "",
-              "| start (us) | items | duration mean / min / max (us) |", "|---|---|---|"]
+              "| start (us) | items | duration mean / min / max (us) |"
+              + (" start to loop, mean us | quarters of the steps, mean us | of which waiting for loads, mean us |"
+                 if has_marks else ""),
+              "|---|---|---|" + ("---|---|---|" if has_marks else "")]
     for lo in np.arange(0, end.max(), 20.0):
         m = full & (start >= lo) & (start < lo + 20.0)
         if m.any():
-            lines.append(f"| {lo:.0f}-{lo + 20:.0f} | {int(m.sum())} | "
-                         f"{dur[m].mean():.1f} / {dur[m].min():.1f} / {dur[m].max():.1f} |")
+            row = (f"| {lo:.0f}-{lo + 20:.0f} | {int(m.sum())} | "
+                   f"{dur[m].mean():.1f} / {dur[m].min():.1f} / {dur[m].max():.1f} |")
+            if has_marks:
+                q = np.diff(np.column_stack([loop0, edges[:, 1:]])[m], axis=1).mean(axis=0)
+                row += f" {(loop0[m] - start[m]).mean():.1f} | " + " / ".join(f"{x:.1f}" for x in q) + " |"
+                if "stall" in rec.dtype.names:
+                    w = (rec["stall"][m].astype(np.float64) / 100.0).mean(axis=0)
+                    row += " " + " / ".join(f"{x:.1f}" for x in w) + " |"
+                else:
+                    row += " - |"
+            lines.append(row)
     xcc = rec["xcc"] & 0xF
     lines += ["", "## Per XCC", "", "| XCC | items | GB | last end (us) |", "|---|---|---|---|"]
     for x in np.unique(xcc):
@@ -117,9 +172,10 @@ def summarize(rec: np.ndarray, case) -> str:
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--shape", default=None, help="a workloads.shape_case spec instead of a configuration")
     ap.add_argument("--out", default=None, help="also write the summary to this file")
     args = ap.parse_args(argv)
-    rec, case = collect(args.config)
+    rec, case = collect(args.config, shape=args.shape)
     text = summarize(rec, case)
     print(text)
     if args.out:
