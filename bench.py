@@ -25,7 +25,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c3_traffic.json")
+# Calibrated HBM bytes per decode launch, one file per configuration (from
+# rocprofv3 FETCH_SIZE / WRITE_SIZE passes; the matching .md gives the commands).
+TRAFFIC_FILES = [os.path.join(ROOT, "profiles", f"decode_c{i}_traffic.json") for i in range(1, 6)]
 ROPE_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "rope_kv_write_traffic.json")
 
 
@@ -634,11 +636,12 @@ def main() -> int:
             log(f"[bench] graph replay unavailable: {exc!r}")
 
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-        if t.get("workload") == case.name:
-            traffic = t.get("bytes_per_launch")
+    for path in TRAFFIC_FILES:
+        if os.path.exists(path):
+            with open(path) as f:
+                t = json.load(f)
+            if t.get("workload") == case.name:
+                traffic = t.get("bytes_per_launch")
 
     peak_read = hbm_probe("read")
     block_bytes = case.block_size * case.kv_heads * case.head_size * case.kv_elem_bytes
