@@ -618,16 +618,24 @@ __device__ __forceinline__ void vm_load16(u32x4& dst, const void* p) {
   asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(dst) : "v"(p));
 }
 
+// K/V cache loads carry the non-temporal hint (nt): every cache byte is read
+// once per call, and streaming reads with nt measured 7.0-7.1 TB/s against
+// 6.1-6.2 TB/s without it (contiguous 4 GiB reads, plain or LDS DMA). On C3
+// the decode kernel went from 217 to 199.5 us.
+__device__ __forceinline__ void vm_load16_kv(u32x4& dst, const void* p) {
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(dst) : "v"(p));
+}
+
 __device__ __forceinline__ void vm_load4(int32_t& dst, const void* p) {
   asm volatile("global_load_dword %0, %1, off" : "=v"(dst) : "v"(p));
 }
 
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
-// (M0 holds the wave-uniform LDS base).
+// (M0 holds the wave-uniform LDS base); K/V cache rows, non-temporal.
 __device__ __forceinline__ void vm_load16_lds(const void* p, uint8_t* lds) {
   const uint32_t base = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds)));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(p), "s"(base) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(p), "s"(base) : "memory", "m0");
 }
 
 // Registers of one in-flight 32-token chunk plus the block IDs of the chunk
@@ -725,7 +733,7 @@ struct MfmaDecoder {
 #pragma unroll
       for (int j = 0; j < kPerRow; ++j) {
         const uint32_t dim = kFp8 ? (j * 64 + g * 16) : (j * 32 + g * 8);
-        vm_load16(b.k[sb * kPerRow + j], p + dim);
+        vm_load16_kv(b.k[sb * kPerRow + j], p + dim);
       }
     }
   }
@@ -746,7 +754,7 @@ struct MfmaDecoder {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t t = c0 + 8 * i + (lane >> 3);
-      vm_load16(b.v[i], vbase + row_of(c0, ids, t, a.v_block, a.v_page) + (lane & 7U) * 16);
+      vm_load16_kv(b.v[i], vbase + row_of(c0, ids, t, a.v_block, a.v_page) + (lane & 7U) * 16);
     }
   }
 
@@ -1156,7 +1164,7 @@ __device__ __forceinline__ void vm_wait_all(u32x4 (&q)[4]) {
 __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, uint8_t* lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds)));
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
 }
 
 __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
