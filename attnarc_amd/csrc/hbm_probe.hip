@@ -7,23 +7,28 @@
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Reads n16 16-byte vectors once (grid-stride) and writes one word per thread
-// so that the loads are not dead.
+// Reads n16 16-byte vectors once with non-temporal loads: workgroup b reads
+// the contiguous range [b * n16 / grid, (b + 1) * n16 / grid), eight loads
+// per thread in flight, and writes one word per thread so that the loads are
+// not dead. (A grid-stride order, each load instruction of the grid 1 KiB
+// apart per wave, measured 6.4 TB/s; contiguous ranges per workgroup 7.0-7.1;
+// the same ranges without the non-temporal hint 6.1-6.2.)
 __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ src, uint64_t n16,
                                                           uint32_t* __restrict__ sink) {
-  const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  const uint64_t lo = n16 * blockIdx.x / gridDim.x;
+  const uint64_t hi = n16 * (blockIdx.x + 1ULL) / gridDim.x;
   u32x4 acc = {0U, 0U, 0U, 0U};
-  uint64_t i = tid;
-  for (; i + 7 * stride < n16; i += 8 * stride) {
+  for (uint64_t i = lo + threadIdx.x; i < hi; i += 8ULL * blockDim.x) {
     u32x4 v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = __builtin_nontemporal_load(&src[i + k * stride]);
+    for (int k = 0; k < 8; ++k) {
+      const uint64_t j = i + static_cast<uint64_t>(k) * blockDim.x;
+      v[k] = j < hi ? __builtin_nontemporal_load(&src[j]) : u32x4{0U, 0U, 0U, 0U};
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) acc ^= v[k];
   }
-  for (; i < n16; i += stride) acc ^= src[i];
-  sink[tid] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  sink[static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
 __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
@@ -79,9 +84,10 @@ extern "C" int loom_hip_probe_slice_read(const void* src, uint64_t bytes, uint32
 
 // Random-chunk gather: the buffer is `chunks` chunks of `chunk_bytes` (a
 // multiple of 16) and workgroup w reads chunks perm[w], perm[w + grid], ...
-// whole, 16 bytes per lane and eight loads per thread in flight. It is the
-// attainable rate of a paged access pattern (K/V blocks scattered by a block
-// table) with no computation. (Spreading each chunk over several workgroups
+// whole, 16 bytes per lane and eight non-temporal loads per thread in
+// flight (as the decode kernels load K/V). It is the attainable rate of a
+// paged access pattern (K/V blocks scattered by a block table) with no
+// computation. (Spreading each chunk over several workgroups
 // measured 0.1-0.2 TB/s slower.)
 __global__ __launch_bounds__(256) void gather_read_kernel(const uint8_t* __restrict__ base,
                                                           const uint32_t* __restrict__ perm, uint32_t chunks,
@@ -95,7 +101,8 @@ __global__ __launch_bounds__(256) void gather_read_kernel(const uint8_t* __restr
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t off = r + (k * blockDim.x + threadIdx.x) * 16U;
-        v[k] = off < chunk_bytes ? *reinterpret_cast<const u32x4*>(p + off) : u32x4{0U, 0U, 0U, 0U};
+        v[k] = off < chunk_bytes ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + off))
+                                 : u32x4{0U, 0U, 0U, 0U};
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) acc ^= v[k];

@@ -197,14 +197,22 @@ __device__ __forceinline__ void put_partial(const DecodeArgs& a, uint64_t idx, f
   }
 }
 
-// Four consecutive dims of one partial row (idx a multiple of 4).
-template <typename QE>
+// Four consecutive dims of one partial row (idx a multiple of 4). kNt: a
+// non-temporal store (the FP8 streaming kernel: C4 decode 199.7 -> 188 us;
+// on the 16-bit streaming kernel it measured 1% slower, C3 199.7 -> 201.5).
+template <typename QE, bool kNt = false>
 __device__ __forceinline__ void put_partial4(const DecodeArgs& a, uint64_t idx, f32x4 o, float scale, float inv_l) {
   if constexpr (PartialOut<QE>::kNormalised) {
     const float k = scale * inv_l;
     const uint32_t w0 = QE::from_f(o[0] * k) | (static_cast<uint32_t>(QE::from_f(o[1] * k)) << 16);
     const uint32_t w1 = QE::from_f(o[2] * k) | (static_cast<uint32_t>(QE::from_f(o[3] * k)) << 16);
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.ws_o) + idx) = make_uint2(w0, w1);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.ws_o) + idx);
+    if constexpr (kNt) {
+      typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+      __builtin_nontemporal_store(u32x2_t{w0, w1}, reinterpret_cast<u32x2_t*>(dst));
+    } else {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
+    }
   } else {
     *reinterpret_cast<float4*>(static_cast<float*>(a.ws_o) + idx) =
         make_float4(o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale);
@@ -1739,7 +1747,7 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
 // (and LSE) when the sequence is one partition, else the partition's
 // partial output (PartialOut encoding) and (m, l) in the split-K workspace. Lane (g, c) holds dims
 // dt*16 + 4g .. +3 of head c; only lanes of live heads call this.
-template <typename QE, typename Dec>
+template <typename QE, bool kNt = false, typename Dec>
 __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec& dec, int ht, uint32_t seq,
                                                   uint32_t head0, uint32_t part, float v_scale, float l) {
   constexpr uint32_t D = Dec::kDt * 16;
@@ -1758,7 +1766,7 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
     const uint64_t state = state_of(a, row, part);
     const float inv_l = 1.0f / l;
 #pragma unroll
-    for (int dt = 0; dt < Dec::kDt; ++dt) put_partial4<QE>(a, state * D + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
+    for (int dt = 0; dt < Dec::kDt; ++dt) put_partial4<QE, kNt>(a, state * D + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
     if (dec.g == 0) {
       a.ws_ml[state * 2] = dec.m[ht];
       a.ws_ml[state * 2 + 1] = l;
@@ -1919,7 +1927,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   if (kSplit == 1) {
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
-      if (ht * 16U + dec.c < a.group) store_wave_result<QE>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
+      if (ht * 16U + dec.c < a.group) store_wave_result<QE, kFp8>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
     }
     return;
   }
@@ -2136,7 +2144,10 @@ constexpr int kStreamGroup = 4;
 // Measured against four: C4 210 -> 205.6 us, head size 64 112.6 -> 108.5,
 // 96 169.7 -> 164.4, 112 104.8 -> 98.6; 16-bit caches measured 1% slower
 // with eight (head size 64) and 6% slower at head size 128 (one workgroup of
-// 128 KiB per CU).
+// 128 KiB per CU). With non-temporal K/V loads and partial stores, four and
+// eight measured the same: C4 decode 189.4-189.9 against 189.6-190.1 us;
+// head size 96: 82.9-84.2 against 79.9-80.3, 112: 89.7-90.2 against
+// 84.9-85.3.
 constexpr int kStreamGroupFp8 = 8;
 
 template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim>

@@ -35,7 +35,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def hbm_probe(kind: str, nbytes: int = 4 << 30, iters: int = 10, per_cu=(4, 8, 16, 32)):
+def hbm_probe(kind: str, nbytes: int = 4 << 30, iters: int = 10, per_cu=(2, 4, 8, 16)):
     """Attainable HBM bandwidth on this box: the best of a streaming read (or
     copy) of ``nbytes`` over grids of ``per_cu`` 256-thread workgroups per CU."""
     import ctypes
