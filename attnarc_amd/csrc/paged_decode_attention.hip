@@ -2144,10 +2144,10 @@ constexpr int kStreamGroup = 4;
 // Measured against four: C4 210 -> 205.6 us, head size 64 112.6 -> 108.5,
 // 96 169.7 -> 164.4, 112 104.8 -> 98.6; 16-bit caches measured 1% slower
 // with eight (head size 64) and 6% slower at head size 128 (one workgroup of
-// 128 KiB per CU). With non-temporal K/V loads and partial stores, four and
-// eight measured the same: C4 decode 189.4-189.9 against 189.6-190.1 us;
-// head size 96: 82.9-84.2 against 79.9-80.3, 112: 89.7-90.2 against
-// 84.9-85.3.
+// 128 KiB per CU). With non-temporal K/V loads and partial stores, four
+// against eight: C4 decode 189.4-189.9 against 189.6-190.1 us (the same);
+// head size 96 82.9-84.2 against 79.9-80.3, 112 89.7-90.2 against 84.9-85.3
+// (eight faster).
 constexpr int kStreamGroupFp8 = 8;
 
 template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim>
