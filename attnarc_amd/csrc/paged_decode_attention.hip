@@ -1169,10 +1169,17 @@ __device__ __forceinline__ void vm_wait_all(u32x4 (&q)[4]) {
   asm volatile("s_waitcnt vmcnt(0)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]) : : "memory");
 }
 
+// kNt: with the non-temporal hint (rows of whole 128-byte lines; see
+// StreamDecoder::kNtKV).
+template <bool kNt>
 __device__ __forceinline__ void vm_load16_lds_sv(uint32_t voff, uint64_t base, uint8_t* lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds)));
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+  if constexpr (kNt) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+  } else {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+  }
 }
 
 __device__ __forceinline__ void scalar_ready(uint32_t& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(v)); }
@@ -1195,6 +1202,14 @@ template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
 struct StreamDecoder {
   static_assert(kD == kDim || kD == 64 || ((kD == 80 || kD == 96 || kD == 112 || kD == 256) && kHT == 1),
                 "head size 64, 128, or 80 / 96 / 112 / 256 with one head tile");
+  // K/V loads carry the non-temporal hint when a cache row is whole 128-byte
+  // lines. Rows that share lines with their neighbours (head sizes 80, 96 and
+  // 112, FP8 at 64-112) then fetch the shared lines twice; measured with the
+  // hint (decode us, one partition of 512, B=64): 16-bit D64 187 -> 170, D128
+  // 187 -> 172, D256 191 -> 176, FP8 D128 104.5 -> 95.5, FP8 D256 121.5 ->
+  // 115, but 16-bit D80 183 -> 206, D96 181 -> 188, D112 167 -> 176, FP8
+  // D64 108 -> 131, D80 118 -> 142, D96 119 -> 130, D112 98 -> 120.
+  static constexpr bool kNtKV = (kD * (kFp8 ? 1U : 2U)) % 128U == 0;
   static constexpr bool kNarrow = kD == 64 && !kFp8;         // 16-bit rows of 128 bytes
   static constexpr bool kF8Narrow = kD == 64 && kFp8;        // FP8 rows of 64 bytes
   static constexpr bool kWide = kD == 256 && !kFp8;          // 16-bit rows of 512 bytes
@@ -1378,41 +1393,41 @@ struct StreamDecoder {
     const uint64_t vb = row_base(vbase, vstride_b, vstride_p, blk, t0);
     if constexpr (kRot) {
 #pragma unroll
-      for (int i = 0; i < kRotDma; ++i) vm_load16_lds_sv(w_voff[i], kb, stage + i * 1024);
+      for (int i = 0; i < kRotDma; ++i) vm_load16_lds_sv<kNtKV>(w_voff[i], kb, stage + i * 1024);
 #pragma unroll
       for (int i = 0; i < kRotDma; ++i)
-        vm_load16_lds_sv(w_voff[kRotDma + i], vb, stage + (kFp8 ? kF8TileBytes : kVOff) + i * 1024);
+        vm_load16_lds_sv<kNtKV>(w_voff[kRotDma + i], vb, stage + (kFp8 ? kF8TileBytes : kVOff) + i * 1024);
     } else if constexpr (kF8Narrow) {
-      vm_load16_lds_sv(f8_k_voff[0], kb, stage);
-      vm_load16_lds_sv(f8_v_voff[0], vb, stage + kF8TileBytes);
+      vm_load16_lds_sv<kNtKV>(f8_k_voff[0], kb, stage);
+      vm_load16_lds_sv<kNtKV>(f8_v_voff[0], vb, stage + kF8TileBytes);
     } else if constexpr (kF8Wide) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(w_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv<kNtKV>(w_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        vm_load16_lds_sv(w_voff[4 + i], vb + 4 * i * vstride_p, stage + kF8TileBytes + i * 1024);
+        vm_load16_lds_sv<kNtKV>(w_voff[4 + i], vb + 4 * i * vstride_p, stage + kF8TileBytes + i * 1024);
     } else if constexpr (kWide) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vm_load16_lds_sv(w_voff[i], kb + 2 * i * kstride_p, stage + i * 1024);
+      for (int i = 0; i < 8; ++i) vm_load16_lds_sv<kNtKV>(w_voff[i], kb + 2 * i * kstride_p, stage + i * 1024);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vm_load16_lds_sv(w_voff[8 + i], vb + 2 * i * vstride_p, stage + kVOff + i * 1024);
+      for (int i = 0; i < 8; ++i) vm_load16_lds_sv<kNtKV>(w_voff[8 + i], vb + 2 * i * vstride_p, stage + kVOff + i * 1024);
     } else if (kNarrow) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
+      for (int i = 0; i < 2; ++i) vm_load16_lds_sv<kNtKV>(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        vm_load16_lds_sv(f8_v_voff[i], vb + 8 * i * vstride_p, stage + kVOff + i * 1024);
+        vm_load16_lds_sv<kNtKV>(f8_v_voff[i], vb + 8 * i * vstride_p, stage + kVOff + i * 1024);
     } else if (kFp8) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) vm_load16_lds_sv(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
+      for (int i = 0; i < 2; ++i) vm_load16_lds_sv<kNtKV>(f8_k_voff[i], kb + 8 * i * kstride_p, stage + i * 1024);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        vm_load16_lds_sv(f8_v_voff[i], vb + 8 * i * vstride_p, stage + kF8TileBytes + i * 1024);
+        vm_load16_lds_sv<kNtKV>(f8_v_voff[i], vb + 8 * i * vstride_p, stage + kF8TileBytes + i * 1024);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(k_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv<kNtKV>(k_voff[i], kb + 4 * i * kstride_p, stage + i * 1024);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vm_load16_lds_sv(v_voff[i & 1], vb + 4 * i * vstride_p, stage + kVOff + i * 1024);
+      for (int i = 0; i < 4; ++i) vm_load16_lds_sv<kNtKV>(v_voff[i & 1], vb + 4 * i * vstride_p, stage + kVOff + i * 1024);
     }
   }
 
@@ -1927,7 +1942,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   if (kSplit == 1) {
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
-      if (ht * 16U + dec.c < a.group) store_wave_result<QE, kFp8>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
+      if (ht * 16U + dec.c < a.group) store_wave_result<QE, kFp8 && Dec::kNtKV>(a, dec, ht, seq, kvh * a.group + ht * 16U, part, v_scale, lt[ht]);
     }
     return;
   }
