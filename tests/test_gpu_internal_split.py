@@ -168,3 +168,20 @@ def test_long_mqa_single_partition_splits_internally():
     expected, want_lse = oracle_expected(case, threads=ORACLE_THREADS)
     assert_parity(out, expected, torch.bfloat16, "long MQA, internal split")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
+@pytest.mark.parametrize("head,hq,hkv,encoding", [
+    (64, 16, 2, "native"), (96, 8, 2, "native"), (112, 8, 2, "fp8"), (256, 8, 2, "native"), (128, 48, 1, "native"),
+    (128, 64, 1, "fp8")])
+def test_internal_split_other_kernels(head, hq, hkv, encoding):
+    """The split runs on every streaming kernel family: head sizes 64, 96,
+    112 and 256, and the wide-group kernel (48 or 64 query heads per KV head)."""
+    case = workloads.make_case(name=f"split_d{head}", dtype=torch.bfloat16, sequences=3, query_heads=hq,
+                               kv_heads=hkv, head_size=head, value_head_size=head, block_size=16,
+                               lengths=[4096, 2500, 2049], seed=head + hq, device=DEV, pool_factor=1.25,
+                               cache_encoding=encoding, layout="HND" if encoding == "fp8" else "NHD")
+    (out, lse), merges = _merges(lambda: workloads.run_case(case, return_lse=True))
+    assert merges == 1 and ops.last_internal_partition_tokens() > 0
+    expected, want_lse = oracle_expected(case, threads=ORACLE_THREADS)
+    assert_parity(out, expected, torch.bfloat16, f"internal split d{head} {hq}/{hkv} {encoding}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
