@@ -1198,7 +1198,8 @@ constexpr int kStreamStagesFp8 = 2;
 // conversion and FP8 rows of 64 bytes come sixteen per instruction; or 256
 // with one head tile (16-bit rows of 512 bytes two per instruction, FP8 rows
 // of 256 bytes four per instruction).
-template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim>
+template <typename QE, bool kFp8, int kHT = 1, uint32_t kD = kDim,
+          int kS = kFp8 ? kStreamStagesFp8 : kStreamStages>
 struct StreamDecoder {
   static_assert(kD == kDim || kD == 64 || ((kD == 80 || kD == 96 || kD == 112 || kD == 256) && kHT == 1),
                 "head size 64, 128, or 80 / 96 / 112 / 256 with one head tile");
@@ -1263,7 +1264,7 @@ struct StreamDecoder {
   // LDS per wave. 16-bit: kStages stages of [K 4 KiB | V 4 KiB]; PV reads V
   // in place. FP8: kStages stages of [K bytes 2 KiB | V bytes 2 KiB], then
   // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
-  static constexpr int kStages = kFp8 ? kStreamStagesFp8 : kStreamStages;
+  static constexpr int kStages = kS;
   static constexpr uint32_t kF8TileBytes = kRot ? kRotDma * 1024 : kStep * kD;  // FP8 bytes of one tensor's step
   static constexpr uint32_t kVOff = kRot ? kRotDma * 1024 : kStep * kPitch;  // 16-bit: V within a stage
   static constexpr uint32_t kStageBytes = kFp8 ? 2 * kF8TileBytes : 2 * kVOff;
@@ -1794,10 +1795,11 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
 // partial-state stores. `tiles` holds kSplit waves' LDS (Dec::kWaveBytes
 // each); after the step loop the same memory holds each wave's O (16 heads x
 // 128 dims F32 = 8 KiB) for the cross-wave reduction.
-template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim>
+template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim,
+          int kS = kFp8 ? kStreamStagesFp8 : kStreamStages>
 __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
   static_assert(kHT == 1 || kSplit == 1, "two head tiles run one wave per item");
-  using Dec = StreamDecoder<QE, kFp8, kHT, kD>;
+  using Dec = StreamDecoder<QE, kFp8, kHT, kD, kS>;
   using vec8 = typename Dec::vec8;
   constexpr int S = Dec::kStages;
   const uint32_t kvh = item.kvh;
@@ -2154,6 +2156,8 @@ void decode_stream_kernel(DecodeArgs a) {
 // requested from one CU at about the same time, which the memory system
 // serves faster than the same rows requested from CUs on different XCDs.
 constexpr int kStreamGroup = 4;
+// Pipeline stages of the grouped kernel's 16-bit waves.
+constexpr int kStreamGroupStages = 2;
 // FP8 caches (rows half as long, stages half as large): eight items per
 // workgroup, which covers all heads of a token row or block when Hkv = 8.
 // Measured against four: C4 210 -> 205.6 us, head size 64 112.6 -> 108.5,
@@ -2168,14 +2172,15 @@ constexpr int kStreamGroupFp8 = 8;
 template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim>
 __global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_group_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8, 1, kD>;
+  constexpr int kGroupStages = kFp8 ? kStreamStagesFp8 : kStreamGroupStages;
+  using Dec = StreamDecoder<QE, kFp8, 1, kD, kGroupStages>;
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * Dec::kWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   LOOM_WAVE_STAMP(blockIdx.x * kGroup + wave);
   const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
   LOOM_WAVE_ITEM(a, item);
   if (!item.valid) return;  // per wave: nothing below waits on the other waves
-  stream_item<QE, kFp8, 1, 1, kD>(a, tiles + wave * Dec::kWaveBytes, item);
+  stream_item<QE, kFp8, 1, 1, kD, kGroupStages>(a, tiles + wave * Dec::kWaveBytes, item);
 }
 
 
