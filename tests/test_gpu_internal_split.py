@@ -185,3 +185,16 @@ def test_internal_split_other_kernels(head, hq, hkv, encoding):
     expected, want_lse = oracle_expected(case, threads=ORACLE_THREADS)
     assert_parity(out, expected, torch.bfloat16, f"internal split d{head} {hq}/{hkv} {encoding}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
+def test_internal_split_on_the_general_kernel():
+    """D != Dv runs on the general (vector) kernel; the split applies there too."""
+    case = workloads.make_case(name="split_vec", dtype=torch.float16, sequences=2, query_heads=8, kv_heads=2,
+                               head_size=128, value_head_size=64, block_size=16, lengths=[3000, 2048], seed=21,
+                               device=DEV, pool_factor=1.25)
+    (out, lse), merges = _merges(lambda: workloads.run_case(case, return_lse=True))
+    assert merges == 1 and ops.last_internal_partition_tokens() > 0
+    assert ops.last_kernel_family() == "vector"
+    expected, want_lse = oracle_expected(case)
+    assert_parity(out, expected, torch.float16, "internal split, general kernel")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
