@@ -84,6 +84,44 @@ def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
     return moved / sec / 1e9
 
 
+PROBE_POLICIES = {0: "plain 16-byte loads", 1: "non-temporal 16-byte loads", 2: "LDS DMA",
+                  3: "LDS DMA, non-temporal"}
+
+
+def policy_probe(policy: int, nbytes: int = 4 << 30, iters: int = 10, per_cu=(2, 4, 8)) -> dict:
+    """Read rate of 4 GiB in contiguous per-workgroup ranges under one load
+    policy (``PROBE_POLICIES``), per grid size; the evidence for the decode
+    kernels' non-temporal K/V loads."""
+    import ctypes
+
+    import torch
+
+    from attnarc_amd import build as _b
+
+    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
+    fn = lib.loom_hip_probe_policy_read
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                   ctypes.c_void_p]
+    props = torch.cuda.get_device_properties(0)
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    sink = torch.empty(props.multi_processor_count * max(per_cu) * 256, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rates = {}
+    for k in per_cu:
+        blocks = props.multi_processor_count * k
+        assert fn(src.data_ptr(), nbytes, sink.data_ptr(), blocks, policy, stream) == 0
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn(src.data_ptr(), nbytes, sink.data_ptr(), blocks, policy, stream)
+        b.record()
+        torch.cuda.synchronize()
+        rates[k] = round(nbytes * iters / (a.elapsed_time(b) * 1e-3) / 1e9, 1)
+    return rates
+
+
 def gather_read_probe(chunk_bytes: int = 16384, nbytes: int = 2 << 30, iters: int = 5,
                       per_cu=(2, 4, 8)) -> float:
     """Attainable rate of a paged access pattern: ``nbytes`` read as randomly
@@ -499,7 +537,7 @@ def main() -> int:
     ap.add_argument("--shape", default=None,
                     help="a decode workload other than the five configurations, e.g. "
                          "'B=64,Hq=16,Hkv=8,D=256,L=2048,part=512' (see workloads.shape_case); not the metric")
-    ap.add_argument("--probe", choices=["read", "copy", "slice"], default=None,
+    ap.add_argument("--probe", choices=["read", "copy", "slice", "policies"], default=None,
                     help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
 
@@ -519,6 +557,11 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.probe == "policies":
+        for policy, name in PROBE_POLICIES.items():
+            print(json.dumps({"probe": "policies", "policy": name, "bytes": 4 << 30,
+                              "GB/s by workgroups per CU": policy_probe(policy)}), flush=True)
+        return 0
     if args.probe == "slice":
         for wgs in (64, 128, 256, 512):
             print(json.dumps({"probe": "slice", "workgroups": wgs, "threads": 512, "bytes": 64 << 20,
