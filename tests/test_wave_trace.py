@@ -41,3 +41,20 @@ def test_split_items_share_their_bytes():
     rec["tokens"] = 512
     text = wave_trace.summarize(rec, case)
     assert f"KV bytes recorded: {512 * 2 * 64 * 2 / 1e9:.4f} GB" in text
+
+
+def test_summary_with_quarter_marks_and_load_waits():
+    case = workloads.make_case(name="trace", dtype=torch.bfloat16, sequences=1, query_heads=8, kv_heads=2,
+                               head_size=64, value_head_size=64, block_size=16, lengths=[1024], seed=1,
+                               device="cpu", pool_factor=1.25, partition_tokens=512)
+    # two full items; loop start 1 us after the start, then four 2 us quarters
+    rec = np.zeros(2, dtype=wave_trace.RECORD_MARKED)
+    rec["t0"] = [0, 0]
+    rec["t1"] = [900, 900]
+    rec["tokens"] = 512
+    rec["part"] = [0, 1]
+    rec["marks"] = [[100, 300, 500, 700], [100, 300, 500, 700]]
+    rec["stall"] = [[10, 20, 30, 40], [10, 20, 30, 40]]
+    text = wave_trace.summarize(rec, case)
+    assert "## Over time, from the quarter marks" in text
+    assert "| 0-20 | 2 | 9.0 / 9.0 / 9.0 | 1.0 | 2.0 / 2.0 / 2.0 / 2.0 | 0.1 / 0.2 / 0.3 / 0.4 |" in text
