@@ -66,6 +66,10 @@ def collect(config: int, warmup: int = 5, shape: str | None = None, prepare=None
     torch.cuda.synchronize()
     if read(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("wave trace read failed")
+    # A single-partition call on a small grid runs split inside the library:
+    # its items are partitions of that size.
+    lib.loom_hip_last_internal_partition_tokens.restype = ctypes.c_uint32
+    case.traced_partition_tokens = int(lib.loom_hip_last_internal_partition_tokens()) or case.partition_tokens
     marks_read = lib.loom_hip_wave_trace_marks_read
     marks_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64]
     marks_read.restype = ctypes.c_int
@@ -99,7 +103,7 @@ def summarize(rec: np.ndarray, case) -> str:
         | rec["kvh"].astype(np.uint64)
     _, inverse, counts = np.unique(key, return_inverse=True, return_counts=True)
     nbytes = rec["tokens"].astype(np.float64) * row_bytes / counts[inverse]
-    full = rec["tokens"] == case.partition_tokens
+    full = rec["tokens"] == getattr(case, "traced_partition_tokens", case.partition_tokens)
     lines = [f"# Wave timeline: {case.name}", "",
              f"- waves with work: {len(rec)}; first start to last end: {end.max():.1f} us",
              f"- KV bytes recorded: {nbytes.sum() / 1e9:.4f} GB (the call's algorithmic bytes: {case.kv_bytes() / 1e9:.4f} GB)",
