@@ -1300,12 +1300,14 @@ struct StreamDecoder {
 
   // Physical block of the step starting at token t0 (clamped to the last
   // active block, so steps past the sequence stay in valid memory).
-  // The value is ready after the next scalar_ready() on it.
+  // A scalar load through the constant address space (the table is not
+  // written during the launch): the compiler issues it where it stands and
+  // waits for it before the value's first use (scalar_ready), so no register
+  // copy or spill can read the destination while the load is in flight.
   __device__ __forceinline__ uint32_t block_of(uint32_t t0) const {
     const uint32_t lb = min(t0 >> a.block_shift, last_block);
-    uint32_t blk;
-    asm volatile("s_load_dword %0, %1, 0x0" : "=s"(blk) : "s"(table + lb));
-    return blk;
+    using ConstWord = const __attribute__((address_space(4))) int32_t;
+    return static_cast<uint32_t>(((ConstWord*)table)[lb]);
   }
 
   __device__ __forceinline__ uint64_t row_base(uint64_t base, uint64_t stride_b, uint64_t stride_p, uint32_t blk,
