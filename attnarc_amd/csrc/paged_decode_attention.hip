@@ -1714,11 +1714,18 @@ __device__ __forceinline__ uint32_t lengths_chunk(const DecodeArgs& a, uint32_t 
   const u32x4s rsrc = {static_cast<uint32_t>(base), static_cast<uint32_t>(base >> 32) & 0xFFFFU, a.sequences * 4U,
                        0x00020000U};
   u32x16 w0, w1, w2, w3;
-  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w0) : "s"(rsrc), "s"(c0 * 4U));
-  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w1) : "s"(rsrc), "s"(c0 * 4U + 64U));
-  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w2) : "s"(rsrc), "s"(c0 * 4U + 128U));
-  asm volatile("s_buffer_load_dwordx16 %0, %1, %2" : "=s"(w3) : "s"(rsrc), "s"(c0 * 4U + 192U));
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(w0), "+s"(w1), "+s"(w2), "+s"(w3));
+  // The loads and their wait in one statement: the words are asm outputs
+  // only once they have arrived, so no register copy or spill can read them
+  // early.
+  asm volatile(
+      "s_buffer_load_dwordx16 %0, %4, %5\n\t"
+      "s_buffer_load_dwordx16 %1, %4, %6\n\t"
+      "s_buffer_load_dwordx16 %2, %4, %7\n\t"
+      "s_buffer_load_dwordx16 %3, %4, %8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(w0), "=&s"(w1), "=&s"(w2), "=&s"(w3)
+      : "s"(rsrc), "s"(c0 * 4U), "s"(c0 * 4U + 64U), "s"(c0 * 4U + 128U), "s"(c0 * 4U + 192U)
+      : "memory");
   uint32_t v = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
