@@ -3164,8 +3164,8 @@ int scratch_address(hipStream_t stream, float** out) {
     return fail(LOOM_HIP_UNAVAILABLE, "no current HIP device");
   }
   // The array's address is the current device's; the launch stream must be
-  // on that device too.
-  if (stream != nullptr) {
+  // on that device too (the null, legacy and per-thread handles always are).
+  if (stream != nullptr && stream != hipStreamLegacy && stream != hipStreamPerThread) {
     hipDevice_t stream_dev = -1;
     if (hipStreamGetDevice(stream, &stream_dev) != hipSuccess) {
       (void)hipGetLastError();

@@ -10,6 +10,8 @@ call left in the shared array leaks into the second.
 
 from __future__ import annotations
 
+import ctypes
+
 import pytest
 import torch
 
@@ -71,3 +73,26 @@ def test_no_alloc_long_mqa_many_partitions():
     small = _case(torch.bfloat16, [5000], seed=76, query_heads=32, kv_heads=1, partition_tokens=1024)
     _check_pair(mqa)
     _check_pair(small)
+
+
+@pytest.mark.parametrize("handle", [1, 2], ids=["legacy", "per-thread"])
+def test_no_alloc_on_special_stream_handles(monkeypatch, handle):
+    """hipStreamLegacy (1) and hipStreamPerThread (2) name streams of the
+    current device: the no-allocation call accepts them like the null stream."""
+    from attnarc_amd import ops
+
+    case = _case(torch.bfloat16, [3000, 900, 4096], seed=77)
+    want_o, want_l = _run(case, no_alloc=False)
+    torch.cuda.synchronize()
+    out = torch.full_like(want_o, float("nan"))
+    lse = torch.full_like(want_l, float("nan"))
+    torch.cuda.synchronize()  # the special stream does not order after torch's stream
+    monkeypatch.setattr(ops, "_stream_handle", lambda device: ctypes.c_void_p(handle))
+    paged_decode_attention_extended(
+        case.query, case.key_cache, case.value_cache, case.block_tables, case.sequence_lengths,
+        max_sequence_length=case.max_sequence_length, scale=case.scale, layout=case.layout,
+        key_scales=case.key_scales, value_scales=case.value_scales, partition_tokens=case.partition_tokens,
+        output=out, lse=lse, no_alloc=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want_o.view(torch.int16))
+    assert torch.equal(lse, want_l)
