@@ -1810,7 +1810,8 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
 // 128 dims F32 = 8 KiB) for the cross-wave reduction.
 template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim,
           int kS = kFp8 ? kStreamStagesFp8 : kStreamStages, int kNt = -1>
-__device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
+__device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item,
+                                            bool preloaded = false, const uint32_t* first_blocks = nullptr) {
   static_assert(kHT == 1 || kSplit == 1, "two head tiles run one wave per item");
   using Dec = StreamDecoder<QE, kFp8, kHT, kD, kS, kNt>;
   using vec8 = typename Dec::vec8;
@@ -1872,12 +1873,20 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     uint32_t nx[S];
     uint32_t bk[S];
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-      tl[i] = tw + i * Dec::kStageBytes;
-      bk[i] = dec.block_of(min(t_first + i * st, t_last));
-    }
+    for (int i = 0; i < S; ++i) tl[i] = tw + i * Dec::kStageBytes;
+    if (preloaded) {
+      // The block IDs of steps 0 .. 2S - 1, loaded with the item's length.
 #pragma unroll
-    for (int i = 0; i < S; ++i) nx[i] = dec.block_of(min(t_first + (S + i) * st, t_last));
+      for (int i = 0; i < S; ++i) {
+        bk[i] = first_blocks[i];
+        nx[i] = first_blocks[S + i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < S; ++i) bk[i] = dec.block_of(min(t_first + i * st, t_last));
+#pragma unroll
+      for (int i = 0; i < S; ++i) nx[i] = dec.block_of(min(t_first + (S + i) * st, t_last));
+    }
 #pragma unroll
     for (int i = 0; i < S; ++i) scalar_ready(bk[i]);
 #pragma unroll
@@ -2183,7 +2192,14 @@ constexpr int kStreamGroupStages = 2;
 // (eight faster).
 constexpr int kStreamGroupFp8 = 8;
 
-template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim, int kNt = -1>
+// kDirect: items in index order (KV head fastest, then partition, then
+// sequence) instead of the longest-first schedule, for the library's own
+// split of small grids, where one round of items covers the launch. The
+// item is known from the index, so its length and its first 2S block IDs
+// are loaded together: the wave starts after two memory round trips, not
+// three. (Compiler-visible scalar loads: the compiler waits for them before
+// any use or copy.)
+template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim, int kNt = -1, bool kDirect = false>
 __global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_group_kernel(DecodeArgs a) {
   constexpr int kGroupStages = kFp8 ? kStreamStagesFp8 : kStreamGroupStages;
@@ -2191,10 +2207,38 @@ void decode_stream_group_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * Dec::kWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   LOOM_WAVE_STAMP(blockIdx.x * kGroup + wave);
-  const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
-  LOOM_WAVE_ITEM(a, item);
-  if (!item.valid) return;  // per wave: nothing below waits on the other waves
-  stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item);
+  if constexpr (kDirect) {
+    const uint32_t bid = blockIdx.x * kGroup + wave;
+    WorkItem item{0, 0, bid % a.kv_heads, 0, false};
+    const uint32_t pair = bid / a.kv_heads;
+    item.seq = pair / a.parts;
+    item.part = pair % a.parts;
+    if (item.seq >= a.sequences) return;
+    // Volatile: issued here, unconditionally and in this order, rather than
+    // moved past the length's wait into the branch that uses them.
+    using ConstWord = const volatile __attribute__((address_space(4))) int32_t;
+    const ConstWord* row = (const ConstWord*)(a.block_tables + static_cast<uint64_t>(item.seq) * a.max_blocks);
+    const uint32_t p0 = item.part * a.partition_tokens;
+    // Steps past the partition's last one clamp onto it; a partition with
+    // fewer than 2S steps, or a sequence ending inside step 2S - 1, takes
+    // the ordinary loads below.
+    const uint32_t t_end = p0 + a.partition_tokens - kStep;
+    uint32_t first[2 * kGroupStages];
+#pragma unroll
+    for (int i = 0; i < 2 * kGroupStages; ++i)
+      first[i] = static_cast<uint32_t>(row[min(min(p0 + i * kStep, t_end) >> a.block_shift, a.max_blocks - 1U)]);
+    item.len = static_cast<uint32_t>(((const ConstWord*)a.sequence_lengths)[item.seq]);
+    if (p0 >= item.len) return;  // per wave: nothing below waits on the other waves
+    item.valid = true;
+    LOOM_WAVE_ITEM(a, item);
+    const bool whole_steps = min(a.partition_tokens, item.len - p0) > (2 * kGroupStages - 1) * kStep;
+    stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item, whole_steps, first);
+  } else {
+    const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
+    LOOM_WAVE_ITEM(a, item);
+    if (!item.valid) return;  // per wave: nothing below waits on the other waves
+    stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item);
+  }
 }
 
 
@@ -2572,6 +2616,7 @@ struct Problem {
   uint32_t partition_tokens;  // 0 = one partition per sequence
   float scale;
   bool static_workspace;  // split-K states go to the library's per-device array
+  bool direct_schedule = false;  // split inside the library: items in index order
 };
 
 size_t elem_size(uint32_t dtype) { return dtype == kF32 ? 4 : 2; }
@@ -2780,11 +2825,11 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
-template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup, int kNt = -1>
+template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup, int kNt = -1, bool kDirect = false>
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   const uint64_t groups = (items + kGroup - 1) / kGroup;
-  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt>), dim3(static_cast<uint32_t>(groups)),
+  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, kDirect>), dim3(static_cast<uint32_t>(groups)),
                      dim3(kGroup * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
@@ -3099,8 +3144,12 @@ int run_typed(const Problem& p, hipStream_t stream) {
       if (group > 16) {
         status = fp8 ? launch_stream<QE, true, 1, 2>(args, grid, stream) : launch_stream<QE, false, 1, 2>(args, grid, stream);
       } else if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
-        status = fp8 ? launch_stream_group<QE, true, kDim, kStreamGroupFp8>(args, grid, stream)
-                     : launch_stream_group<QE, false>(args, grid, stream);
+        // The library's own split runs its items in index order with each
+        // item's first block IDs loaded alongside its length (C2 decode
+        // 18.3-18.5 -> 17.5-17.7 us).
+        status = fp8                  ? launch_stream_group<QE, true, kDim, kStreamGroupFp8>(args, grid, stream)
+                 : p.direct_schedule ? launch_stream_group<QE, false, kDim, kStreamGroup, -1, true>(args, grid, stream)
+                                     : launch_stream_group<QE, false>(args, grid, stream);
       } else if (steps < 8) {
         status = fp8 ? launch_stream<QE, true, 1>(args, grid, stream) : launch_stream<QE, false, 1>(args, grid, stream);
       } else {
@@ -3316,6 +3365,7 @@ int run(Problem p, void* stream) {
       p.partition_tokens = t;
       p.workspace = slot;
       p.workspace_elements = kPoolSlotElements;
+      p.direct_schedule = true;
       internal = t;
     }
   }

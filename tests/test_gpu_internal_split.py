@@ -102,6 +102,22 @@ def test_environment_switch_keeps_one_partition(no_internal_split):
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
+def test_index_order_split_with_ragged_partition_tails():
+    """The library's own split of a 16-bit D=128 grid of 1024 items runs its
+    items in index order and loads each item's first four block IDs with its
+    length; a last partition of 48 tokens or fewer takes the ordinary loads.
+    Tails of 0-255 tokens (1, 16, 48, 49, ...), one-token sequences and items
+    past a sequence's end, against the oracle."""
+    lengths = (4096, 2049, 2064, 2096, 2097, 1, 17, 300, 3333, 256, 257, 304, 4095, 1000, 2500, 3900)
+    case = _case(21, lengths=lengths, hq=32, hkv=4)
+    (out, lse), merges = _merges(lambda: workloads.run_case(case, return_lse=True))
+    assert merges == 1
+    assert ops.last_internal_partition_tokens() == 256  # 16 partitions x 64 items: 1024 grouped items
+    expected, want_lse = oracle_expected(case)
+    assert_parity(out, expected, torch.bfloat16, "index-order internal split, ragged tails")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
 def test_large_grid_or_short_context_stays_whole():
     short = _case(14, lengths=(2047, 700, 999, 512))  # contexts under 2048 stay whole
     _, merges = _merges(lambda: workloads.run_case(short))
