@@ -2159,6 +2159,40 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
   }
 }
 
+// Item bid in index order (KV head fastest, then partition, then sequence;
+// valid = false for a partition past its sequence's end), with the block IDs
+// of the item's first kN steps loaded together with its length. preloaded
+// tells whether they are the ones the item uses: a partition with fewer than
+// kN steps, or a sequence ending inside step kN - 1, takes the ordinary
+// loads. Volatile constant-address-space scalar loads: the compiler issues
+// them here, unconditionally and in order, and waits for them before any use
+// or copy.
+template <int kN>
+__device__ __forceinline__ WorkItem direct_item(const DecodeArgs& a, uint32_t bid, uint32_t (&first)[kN],
+                                                bool& preloaded) {
+  WorkItem item{0, 0, bid % a.kv_heads, 0, false};
+  const uint32_t pair = bid / a.kv_heads;
+  item.seq = pair / a.parts;
+  item.part = pair % a.parts;
+  preloaded = false;
+  if (item.seq >= a.sequences) return item;
+  using ConstWord = const volatile __attribute__((address_space(4))) int32_t;
+  const ConstWord* row = (const ConstWord*)(a.block_tables + static_cast<uint64_t>(item.seq) * a.max_blocks);
+  const ConstWord* lens = (const ConstWord*)a.sequence_lengths;
+  const uint32_t p0 = item.part * a.partition_tokens;
+  const uint32_t t_end = p0 + a.partition_tokens - kStep;  // steps past the last one clamp onto it
+  uint32_t at[kN];
+#pragma unroll
+  for (int i = 0; i < kN; ++i) at[i] = min(min(p0 + i * kStep, t_end) >> a.block_shift, a.max_blocks - 1U);
+  item.len = static_cast<uint32_t>(lens[item.seq]);  // first: its address needs nothing loaded
+#pragma unroll
+  for (int i = 0; i < kN; ++i) first[i] = static_cast<uint32_t>(row[at[i]]);
+  if (p0 >= item.len) return item;
+  item.valid = true;
+  preloaded = min(a.partition_tokens, item.len - p0) > (kN - 1) * kStep;
+  return item;
+}
+
 template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim, int kNt = -1>
 __global__ __launch_bounds__(kSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_kernel(DecodeArgs a) {
@@ -2208,31 +2242,12 @@ void decode_stream_group_kernel(DecodeArgs a) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   LOOM_WAVE_STAMP(blockIdx.x * kGroup + wave);
   if constexpr (kDirect) {
-    const uint32_t bid = blockIdx.x * kGroup + wave;
-    WorkItem item{0, 0, bid % a.kv_heads, 0, false};
-    const uint32_t pair = bid / a.kv_heads;
-    item.seq = pair / a.parts;
-    item.part = pair % a.parts;
-    if (item.seq >= a.sequences) return;
-    // Volatile: issued here, unconditionally and in this order, rather than
-    // moved past the length's wait into the branch that uses them.
-    using ConstWord = const volatile __attribute__((address_space(4))) int32_t;
-    const ConstWord* row = (const ConstWord*)(a.block_tables + static_cast<uint64_t>(item.seq) * a.max_blocks);
-    const uint32_t p0 = item.part * a.partition_tokens;
-    // Steps past the partition's last one clamp onto it; a partition with
-    // fewer than 2S steps, or a sequence ending inside step 2S - 1, takes
-    // the ordinary loads below.
-    const uint32_t t_end = p0 + a.partition_tokens - kStep;
     uint32_t first[2 * kGroupStages];
-#pragma unroll
-    for (int i = 0; i < 2 * kGroupStages; ++i)
-      first[i] = static_cast<uint32_t>(row[min(min(p0 + i * kStep, t_end) >> a.block_shift, a.max_blocks - 1U)]);
-    item.len = static_cast<uint32_t>(((const ConstWord*)a.sequence_lengths)[item.seq]);
-    if (p0 >= item.len) return;  // per wave: nothing below waits on the other waves
-    item.valid = true;
+    bool preloaded = false;
+    const WorkItem item = direct_item<2 * kGroupStages>(a, blockIdx.x * kGroup + wave, first, preloaded);
+    if (!item.valid) return;  // per wave: nothing below waits on the other waves
     LOOM_WAVE_ITEM(a, item);
-    const bool whole_steps = min(a.partition_tokens, item.len - p0) > (2 * kGroupStages - 1) * kStep;
-    stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item, whole_steps, first);
+    stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item, preloaded, first);
   } else {
     const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
     LOOM_WAVE_ITEM(a, item);
