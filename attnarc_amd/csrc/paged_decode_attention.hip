@@ -1164,6 +1164,23 @@ __device__ __forceinline__ void vm_wait_dma() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
+// Waits for a step's DMA while the loads of min(later, kMax) later steps
+// (kPer instructions each) stay in flight. `later` is wave-uniform: the
+// steps issued after the awaited one, fewer than kMax near an item's end,
+// where no load is issued past the item's last step.
+template <int kPer, int kMax>
+__device__ __forceinline__ void vm_wait_dma_later(uint32_t later) {
+  if constexpr (kMax <= 0) {
+    vm_wait_dma<0>();
+  } else {
+    if (later >= static_cast<uint32_t>(kMax)) {
+      vm_wait_dma<kPer * kMax>();
+    } else {
+      vm_wait_dma_later<kPer, kMax - 1>(later);
+    }
+  }
+}
+
 // Waits for the query registers as well (loaded after the K/V DMA).
 __device__ __forceinline__ void vm_wait_all(u32x4 (&q)[4]) {
   asm volatile("s_waitcnt vmcnt(0)" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]) : : "memory");
@@ -1851,8 +1868,8 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
   dec.sl2 = a.score_scale_log2 * k_scale;
 
   // Steps of this partition: step k covers [p0 + 16k, p0 + 16k + 16); wave
-  // w takes steps w, w + kSplit, ...; steps past the wave's last one are
-  // clamped onto it (re-reads that hit in cache), keeping the issue uniform.
+  // w takes steps w, w + kSplit, ... Block-table reads past the wave's last
+  // step are clamped onto it; no K/V load is issued past it.
   const uint32_t nst = (dec.p1 - p0 + kStep - 1) / kStep;
   const uint32_t my_n = nst > wave ? (nst - wave + kSplit - 1) / kSplit : 0;
   const uint32_t st = kSplit * kStep;
@@ -1890,7 +1907,9 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
 #pragma unroll
     for (int i = 0; i < S; ++i) scalar_ready(bk[i]);
 #pragma unroll
-    for (int i = 0; i < S; ++i) dec.issue(tl[i], bk[i], min(t_first + i * st, t_last));
+    for (int i = 0; i < S; ++i) {
+      if (i < my_n) dec.issue(tl[i], bk[i], t_first + i * st);
+    }
     // Q is loaded after the first steps' K/V and waited for together with
     // them, so a wave's start costs one memory round trip, not two.
     {
@@ -1930,10 +1949,9 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       for (int i = 0; i < S; ++i) {
         if (n + i < my_n) {
           const uint32_t t0 = t_first + (n + i) * st;
-          const uint32_t tn = min(t0 + S * st, t_last);
           uint8_t* vtile = kFp8 ? tw + Dec::kVTileOff : tl[i] + Dec::kVOff;
-          // this step's loads; S - 1 steps stay in flight
-          LOOM_WAVE_STALL(n + i, my_n, (vm_wait_dma<Dec::kDmaPerStep * (S - 1)>()));
+          // this step's loads; the later steps' (up to S - 1) stay in flight
+          LOOM_WAVE_STALL(n + i, my_n, (vm_wait_dma_later<Dec::kDmaPerStep, S - 1>(my_n - 1 - (n + i))));
           scalar_ready(nx[i]);
           if (kFp8) {
             dec.stage_v_fp8(tl[i], vtile, t0);
@@ -1945,7 +1963,9 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
           dec.qk(tl[i], sc);
           dec.softmax_pv(sc, t0, vtile);
           wait_lds_reads();
-          dec.issue(tl[i], nx[i], tn);
+          // No load past the item's last step: such a load would re-read
+          // rows nobody consumes, and the wave's exit would wait for it.
+          if (n + i + S < my_n) dec.issue(tl[i], nx[i], t0 + S * st);
           wave_fence_lds();
           nx[i] = dec.block_of(min(t0 + 2 * S * st, t_last));
         }
@@ -2076,8 +2096,9 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
 
   const uint32_t nst = (dec.p1 - p0 + kStep - 1) / kStep;  // >= 1: the item holds tokens
   const uint32_t t_last = p0 + (nst - 1) * kStep;
-  // nx[j]: block of the next step that wave 0 loads into stage j (steps past
-  // the item's last are clamped onto it: cache hits, keeping the issue uniform).
+  // nx[j]: block of the next step that wave 0 loads into stage j (table
+  // reads past the item's last step are clamped onto it; no K/V load is
+  // issued past it).
   uint32_t nx[S];
   if (wave == 0) {
     uint32_t bk[S - 1];
@@ -2089,7 +2110,9 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
 #pragma unroll
     for (int i = 0; i < S - 1; ++i) scalar_ready(bk[i]);
 #pragma unroll
-    for (int i = 0; i < S - 1; ++i) dec.issue(tiles + i * Dec::kStageBytes, bk[i], min(p0 + i * kStep, t_last));
+    for (int i = 0; i < S - 1; ++i) {
+      if (i < nst) dec.issue(tiles + i * Dec::kStageBytes, bk[i], p0 + i * kStep);
+    }
   }
   {
     u32x4 qw[2][Dec::kKc];
@@ -2127,13 +2150,14 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
         uint8_t* stage = tiles + i * Dec::kStageBytes;
         const int j = (i + S - 1) % S;  // the stage of the previous step
         if (wave == 0) {
-          vm_wait_dma<Dec::kDmaPerStep * (S - 2)>();  // this step's loads; S - 2 later steps stay in flight
+          // this step's loads; the later steps' (up to S - 2) stay in flight
+          vm_wait_dma_later<Dec::kDmaPerStep, S - 2>(nst - 1 - (n + i));
           if (!kFp8) dec.zero_dead_rows(stage + Dec::kVOff, t0);
         }
         lds_barrier();  // this step's stage is in LDS; every wave is done with the previous one
         if (wave == 0) {
           scalar_ready(nx[j]);
-          dec.issue(tiles + j * Dec::kStageBytes, nx[j], min(t0 + (S - 1) * kStep, t_last));
+          if (n + i + S - 1 < nst) dec.issue(tiles + j * Dec::kStageBytes, nx[j], t0 + (S - 1) * kStep);
           nx[j] = dec.block_of(min(t0 + (2 * S - 1) * kStep, t_last));
         }
         uint8_t* vtile = kFp8 ? vconv : stage + Dec::kVOff;
