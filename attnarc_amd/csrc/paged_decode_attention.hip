@@ -25,7 +25,7 @@
 //                        that are not a multiple of 16 tokens.
 //   decode_vector_kernel any shape and dtype (including F32); fp32 VALU on
 //                        64-token tiles. Covers the general contract.
-//   merge_kernel / merge_rows128_kernel / merge_wide_kernel
+//   merge_kernel / merge_rows_kernel / merge_wide_kernel
 //                        stable log-sum-exp merge of per-partition states
 //                        (the math of paged_decode_attention.cu:780-852).
 //
@@ -78,7 +78,7 @@ struct DecodeArgs {
   void* output;
   float* lse;
   float* ws_ml;  // [sequences][parts][query_heads][2] = (m in log2 units, l)
-  void* ws_o;    // [sequences][parts][query_heads][Dv] partial outputs (PartialOut<QE> encoding)
+  float* ws_o;   // [sequences][parts][query_heads][Dv] partial outputs (F32 sums, put_partial)
   uint64_t k_block, k_page, k_head;  // element strides of the key cache
   uint64_t v_block, v_page, v_head;  // element strides of the value cache
   uint32_t query_heads;
@@ -165,57 +165,26 @@ __device__ __forceinline__ void wave_fence_lds() { asm volatile("" ::: "memory")
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maxima).
 __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Split-K partial outputs. F32 queries keep the unnormalised F32 sum
-// O_p = sum_t 2^(s_t - m_p) v_t. 16-bit queries store o_p = O_p / l_p in the
-// query's own type: half the bytes of the (write-heavy) partial states, and
-// o_p is a convex combination of V rows, so it stays in range; the merge
-// weights it by l_p again. The workspace keeps its F32 element count.
-template <typename QE>
-struct PartialOut {
-  static constexpr bool kNormalised = true;
-  using T = uint16_t;
-};
-template <>
-struct PartialOut<F32Elem> {
-  static constexpr bool kNormalised = false;
-  using T = float;
-};
-
-// Elements between consecutive partial rows: Dv, rounded up to even for
-// 16-bit partials so the merge can read dim pairs as aligned 4-byte words.
-template <typename QE>
-__host__ __device__ __forceinline__ uint32_t partial_stride(uint32_t dv) {
-  return PartialOut<QE>::kNormalised ? (dv + 1U) & ~1U : dv;
+// Split-K partial outputs: the unnormalised F32 sum O_p = sum_t 2^(s_t -
+// m_p) v_t (times the FP8 value scale) of each partition, as the reference
+// keeps them (paged_decode_attention.cu:683-702): every output is rounded to
+// its storage type once, by the merge. (16-bit o_p = O_p / l_p partials,
+// half the bytes, were measured against the oracle: a partial rounded to
+// BF16 carries up to half an ulp of |o_p|, which a merge of partials of
+// opposite sign keeps in full, up to 7.8e-3 on 16-token partitions.)
+__device__ __forceinline__ void put_partial(const DecodeArgs& a, uint64_t idx, float o) {
+  static_cast<float*>(a.ws_o)[idx] = o;
 }
 
-template <typename QE>
-__device__ __forceinline__ void put_partial(const DecodeArgs& a, uint64_t idx, float o, float inv_l) {
-  if constexpr (PartialOut<QE>::kNormalised) {
-    static_cast<uint16_t*>(a.ws_o)[idx] = QE::from_f(o * inv_l);
+// Four consecutive dims of one partial row (idx a multiple of 4), times
+// scale. kNt: a non-temporal store.
+template <bool kNt = false>
+__device__ __forceinline__ void put_partial4(const DecodeArgs& a, uint64_t idx, f32x4 o, float scale) {
+  f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(a.ws_o) + idx);
+  if constexpr (kNt) {
+    __builtin_nontemporal_store(o * scale, dst);
   } else {
-    static_cast<float*>(a.ws_o)[idx] = o;
-  }
-}
-
-// Four consecutive dims of one partial row (idx a multiple of 4). kNt: a
-// non-temporal store (the FP8 streaming kernel: C4 decode 199.7 -> 188 us;
-// on the 16-bit streaming kernel it measured 1% slower, C3 199.7 -> 201.5).
-template <typename QE, bool kNt = false>
-__device__ __forceinline__ void put_partial4(const DecodeArgs& a, uint64_t idx, f32x4 o, float scale, float inv_l) {
-  if constexpr (PartialOut<QE>::kNormalised) {
-    const float k = scale * inv_l;
-    const uint32_t w0 = QE::from_f(o[0] * k) | (static_cast<uint32_t>(QE::from_f(o[1] * k)) << 16);
-    const uint32_t w1 = QE::from_f(o[2] * k) | (static_cast<uint32_t>(QE::from_f(o[3] * k)) << 16);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.ws_o) + idx);
-    if constexpr (kNt) {
-      typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-      __builtin_nontemporal_store(u32x2_t{w0, w1}, reinterpret_cast<u32x2_t*>(dst));
-    } else {
-      *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
-    }
-  } else {
-    *reinterpret_cast<float4*>(static_cast<float*>(a.ws_o) + idx) =
-        make_float4(o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale);
+    *dst = o * scale;
   }
 }
 
@@ -536,7 +505,7 @@ __global__ __launch_bounds__(kVecThreads) void decode_vector_kernel(DecodeArgs a
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
       const uint64_t state = state_of(a, row, part);
-      put_partial<QE>(a, state * partial_stride<QE>(Dv) + d, O, 1.0f / L);
+      put_partial(a, state * Dv + d, O);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
         a.ws_ml[state * 2 + 1] = L;
@@ -582,6 +551,17 @@ struct MfmaOps<Bf16Elem> {
     const bf16x2 v{static_cast<__bf16>(x), static_cast<__bf16>(y)};
     return __builtin_bit_cast(uint32_t, v);
   }
+  // PV takes the probabilities as a BF16 pair hi + lo: BF16's 8 significant
+  // bits alone put up to 2^-9 of relative error on every weight, which a row
+  // of large values of opposite sign keeps in full (measured 3.9e-3 against
+  // the oracle on a 16-token head-256 row, past the 2e-3 parity bar). The
+  // remainder x - hi rides in the same MFMA where the product has room for
+  // it (StreamDecoder: one K = 32 instruction in place of K = 16), else in a
+  // second one.
+  static constexpr bool kSplitP = true;
+  static __device__ __forceinline__ uint32_t rest2(float x, float y, uint32_t hi) {
+    return pack2(x - __uint_as_float(hi << 16), y - __uint_as_float(hi & 0xFFFF0000U));
+  }
 };
 
 template <>
@@ -605,6 +585,9 @@ struct MfmaOps<F16Elem> {
     const f16x2 v{static_cast<_Float16>(x), static_cast<_Float16>(y)};
     return __builtin_bit_cast(uint32_t, v);
   }
+  // F16 probabilities keep 11 significant bits (P <= 1): one MFMA.
+  static constexpr bool kSplitP = false;
+  static __device__ __forceinline__ uint32_t rest2(float, float, uint32_t) { return 0U; }
 };
 
 __device__ __forceinline__ u32x4 load16(const void* p) {
@@ -838,7 +821,7 @@ struct MfmaDecoder {
 
   // Online softmax and PV of one chunk whose V is in `tile`.
   __device__ __forceinline__ void softmax_pv(f32x4 (&s)[kHeadTiles][2], uint32_t c0, const uint8_t* tile) {
-    vec8 pb[kHeadTiles];
+    vec8 pb[kHeadTiles], pr[kHeadTiles];
 #pragma unroll
     for (int ht = 0; ht < kHeadTiles; ++ht) {
       float cmax = -INFINITY;
@@ -873,12 +856,20 @@ struct MfmaDecoder {
       w[2] = Ops::pack2(p[4], p[5]);
       w[3] = Ops::pack2(p[6], p[7]);
       pb[ht] = __builtin_bit_cast(vec8, w);
+      if constexpr (Ops::kSplitP) {
+        const u32x4 r{Ops::rest2(p[0], p[1], w[0]), Ops::rest2(p[2], p[3], w[1]), Ops::rest2(p[4], p[5], w[2]),
+                      Ops::rest2(p[6], p[7], w[3])};
+        pr[ht] = __builtin_bit_cast(vec8, r);
+      }
     }
 #pragma unroll
     for (uint32_t dt = 0; dt < 8; ++dt) {
       const vec8 va = v_operand(tile, dt);
 #pragma unroll
-      for (int ht = 0; ht < kHeadTiles; ++ht) acc[ht][dt] = Ops::mma(va, pb[ht], acc[ht][dt]);
+      for (int ht = 0; ht < kHeadTiles; ++ht) {
+        acc[ht][dt] = Ops::mma(va, pb[ht], acc[ht][dt]);
+        if constexpr (Ops::kSplitP) acc[ht][dt] = Ops::mma(va, pr[ht], acc[ht][dt]);
+      }
     }
   }
 
@@ -941,7 +932,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
   dec.table = a.block_tables + static_cast<uint64_t>(seq) * a.max_blocks;
   dec.kbase = static_cast<const CT*>(a.key_cache) + static_cast<uint64_t>(kvh) * a.k_head;
   dec.vbase = static_cast<const CT*>(a.value_cache) + static_cast<uint64_t>(kvh) * a.v_head;
-  const uint32_t wave = kWaves == 1 ? 0U : (threadIdx.x >> 6);
+  const uint32_t wave = kWaves == 1 ? 0U : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t* tA = tile0 + wave * kTileBytes;
   uint8_t* tB = tile1 + wave * kTileBytes;
 
@@ -1046,10 +1037,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
         if (a.lse != nullptr && dec.g == 0) a.lse[row] = (M + log2f(L)) * kLn2;
       } else {
         const uint64_t state = state_of(a, row, part);
-        const float inv_l = 1.0f / L;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-          put_partial4<QE>(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
+        for (int dt = 0; dt < 8; ++dt) put_partial4(a, state * kDim + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale);
         if (dec.g == 0) {
           a.ws_ml[state * 2] = M;
           a.ws_ml[state * 2 + 1] = L;
@@ -1099,7 +1088,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_mfma_kernel(DecodeArgs a) 
         if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
       } else {
         const uint64_t state = state_of(a, row, part);
-        put_partial<QE>(a, state * kDim + d, O, 1.0f / L);
+        put_partial(a, state * kDim + d, O);
         if (d == 0) {
           a.ws_ml[state * 2] = M;
           a.ws_ml[state * 2 + 1] = L;
@@ -1282,6 +1271,12 @@ struct StreamDecoder {
   using Ops = MfmaOps<QE>;
   using vec8 = typename Ops::vec8;
   using vec4 = typename Ops::vec4;
+  // PV's element type: the query's for 16-bit caches; F16 for FP8 caches,
+  // whose E4M3 values convert to F16 exactly and whose probabilities then
+  // keep 11 significant bits in one MFMA (BF16 ones need a hi + lo pair).
+  using PvOps = std::conditional_t<kFp8, MfmaOps<F16Elem>, Ops>;
+  using pv8 = typename PvOps::vec8;
+  using pv4 = typename PvOps::vec4;
   // LDS per wave. 16-bit: kStages stages of [K 4 KiB | V 4 KiB]; PV reads V
   // in place. FP8: kStages stages of [K bytes 2 KiB | V bytes 2 KiB], then
   // one 4 KiB tile of the current step's V converted to 16 bits (kVTileOff).
@@ -1518,12 +1513,12 @@ struct StreamDecoder {
           const uint32_t t = idx / kSrcChunks, lc = idx % kSrcChunks;
           const u32x4 raw = *reinterpret_cast<const u32x4*>(stage + kF8TileBytes + t * kD + lc * 16);
           const u32x4 w = t0 + t < len ? raw : u32x4{0U, 0U, 0U, 0U};
-          const vec8 lo = Ops::from_fp8(w[0], w[1]), hi = Ops::from_fp8(w[2], w[3]);
+          const pv8 lo = PvOps::from_fp8(w[0], w[1]), hi = PvOps::from_fp8(w[2], w[3]);
           // Lanes 4..7 of each eight store their upper chunk first, which
           // spreads each store's eight lanes over distinct bank quarters.
           const uint32_t up = (lane >> 2) & 1U;
-          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc + up)) = up ? hi : lo;
-          *reinterpret_cast<vec8*>(tile + vt_off(t, 2 * lc + 1 - up)) = up ? lo : hi;
+          *reinterpret_cast<pv8*>(tile + vt_off(t, 2 * lc + up)) = up ? hi : lo;
+          *reinterpret_cast<pv8*>(tile + vt_off(t, 2 * lc + 1 - up)) = up ? lo : hi;
         }
       }
       return;
@@ -1544,10 +1539,10 @@ struct StreamDecoder {
       const u32x4 raw = *reinterpret_cast<const u32x4*>(vrow + ((lc ^ swz) << 4));
       const u32x4 w = live ? raw : u32x4{0U, 0U, 0U, 0U};
       // 16-bit chunks 2 lc and 2 lc + 1 (8 dims each).
-      const vec8 lo = Ops::from_fp8(w[0], w[1]), hi = Ops::from_fp8(w[2], w[3]);
+      const pv8 lo = PvOps::from_fp8(w[0], w[1]), hi = PvOps::from_fp8(w[2], w[3]);
       const uint32_t ch = lc * 2;
-      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + up)) = up ? hi : lo;
-      *reinterpret_cast<vec8*>(tile + vtile_off<kPitch>(t, ch + 1 - up)) = up ? lo : hi;
+      *reinterpret_cast<pv8*>(tile + vtile_off<kPitch>(t, ch + up)) = up ? hi : lo;
+      *reinterpret_cast<pv8*>(tile + vtile_off<kPitch>(t, ch + 1 - up)) = up ? lo : hi;
     }
   }
 
@@ -1572,7 +1567,7 @@ struct StreamDecoder {
 
   __device__ __forceinline__ void softmax_pv(f32x4 (&s)[kHT], uint32_t t0, const uint8_t* tile) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    vec4 pb[kHT];
+    pv4 pb[kHT], pr[kHT];
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
       float cmax = -INFINITY;
@@ -1599,8 +1594,10 @@ struct StreamDecoder {
         p[r] = __builtin_amdgcn_exp2f(s[ht][r] - m[ht]);
         lsum[ht] += p[r];
       }
-      const uint32_t w0 = Ops::pack2(p[0], p[1]), w1 = Ops::pack2(p[2], p[3]);
-      pb[ht] = __builtin_bit_cast(vec4, u32x2{w0, w1});
+      const uint32_t w0 = PvOps::pack2(p[0], p[1]), w1 = PvOps::pack2(p[2], p[3]);
+      pb[ht] = __builtin_bit_cast(pv4, u32x2{w0, w1});
+      if constexpr (PvOps::kSplitP)
+        pr[ht] = __builtin_bit_cast(pv4, u32x2{PvOps::rest2(p[0], p[1], w0), PvOps::rest2(p[2], p[3], w1)});
     }
     const uint32_t k = c >> 2, q = c & 3U;
     lds_u8* base = (lds_u8*)tile;
@@ -1609,7 +1606,20 @@ struct StreamDecoder {
       const uint32_t off = vt_off(4 * g + k, 2 * dt + (q >> 1)) + (q & 1U) * 8;
       const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + off));
 #pragma unroll
-      for (int ht = 0; ht < kHT; ++ht) acc[ht][dt] = Ops::mma16(__builtin_bit_cast(vec4, va), pb[ht], acc[ht][dt]);
+      for (int ht = 0; ht < kHT; ++ht) {
+        if constexpr (PvOps::kSplitP) {
+          // One K = 32 MFMA: K index 8g + r pairs token 4g + r with hi, 8g + 4 + r
+          // with its remainder lo; the V operand repeats the lane's four tokens.
+          typedef short s16x8 __attribute__((ext_vector_type(8)));
+          const s16x4 v4 = __builtin_bit_cast(s16x4, va);
+          const s16x4 h4 = __builtin_bit_cast(s16x4, pb[ht]), l4 = __builtin_bit_cast(s16x4, pr[ht]);
+          const s16x8 a8 = __builtin_shufflevector(v4, v4, 0, 1, 2, 3, 0, 1, 2, 3);
+          const s16x8 b8 = __builtin_shufflevector(h4, l4, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[ht][dt] = PvOps::mma(__builtin_bit_cast(pv8, a8), __builtin_bit_cast(pv8, b8), acc[ht][dt]);
+        } else {
+          acc[ht][dt] = PvOps::mma16(__builtin_bit_cast(pv4, va), pb[ht], acc[ht][dt]);
+        }
+      }
     }
   }
 };
@@ -1767,7 +1777,11 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   for (int cls = 0; cls < 2; ++cls) {
 #pragma unroll 1
     for (uint32_t c0 = 0; c0 < a.sequences; c0 += 64) {
-      const uint32_t len = lengths_chunk(a, c0, lane);
+      // A length past the launch's partitions (a caller breaking the
+      // max_sequence_length contract) is clamped to them, so no item
+      // addresses a state or a table entry outside its sequence's share.
+      const uint32_t len = static_cast<uint32_t>(min(static_cast<uint64_t>(lengths_chunk(a, c0, lane)),
+                                                     static_cast<uint64_t>(a.parts) * pt));
       const uint32_t full = len / pt;
       const uint32_t n = cls == 0 ? full : (len % pt != 0 ? 1U : 0U);
       const uint32_t incl = wave_inclusive_sum(n, lane);
@@ -1791,7 +1805,7 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
 
 // One wave's result for its KV head's query group: the normalised output
 // (and LSE) when the sequence is one partition, else the partition's
-// partial output (PartialOut encoding) and (m, l) in the split-K workspace. Lane (g, c) holds dims
+// partial output (F32 sum) and (m, l) in the split-K workspace. Lane (g, c) holds dims
 // dt*16 + 4g .. +3 of head c; only lanes of live heads call this.
 template <typename QE, bool kNt = false, typename Dec>
 __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec& dec, int ht, uint32_t seq,
@@ -1810,14 +1824,106 @@ __device__ __forceinline__ void store_wave_result(const DecodeArgs& a, const Dec
     if (a.lse != nullptr && dec.g == 0) a.lse[row] = (dec.m[ht] + log2f(l)) * kLn2;
   } else {
     const uint64_t state = state_of(a, row, part);
-    const float inv_l = 1.0f / l;
 #pragma unroll
-    for (int dt = 0; dt < Dec::kDt; ++dt) put_partial4<QE, kNt>(a, state * D + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale, inv_l);
+    for (int dt = 0; dt < Dec::kDt; ++dt) put_partial4<kNt>(a, state * D + 4 * dec.g + dt * 16, dec.acc[ht][dt], v_scale);
     if (dec.g == 0) {
       a.ws_ml[state * 2] = dec.m[ht];
       a.ws_ml[state * 2 + 1] = l;
     }
   }
+}
+
+
+// Merge state of one lane: the running maximum M (log2 units), the sum L
+// and dims 4c .. 4c + 3 of the weighted partial sums.
+struct MergeState {
+  float m, l;
+  f32x4 o;
+};
+
+// Combines two merge states by the log-sum-exp identity (a state without
+// partitions has m = -inf and weight 0).
+__device__ __forceinline__ MergeState merge_combine(const MergeState& x, const MergeState& y) {
+  const float m = fmaxf(x.m, y.m);
+  const float fx = isfinite(x.m) ? exp2f(x.m - m) : 0.0f;
+  const float fy = isfinite(y.m) ? exp2f(y.m - m) : 0.0f;
+  return MergeState{m, x.l * fx + y.l * fy, x.o * fx + y.o * fy};
+}
+
+// One wave's merge of the partitions first, first + stride, ... (below n)
+// of the row whose partition 0 is state s0 (partition p: state s0 + p *
+// query_heads), Dv = kD (64, 128 or 256) F32 partial rows, 16-byte aligned.
+// Lane (q, c) reads dims 4c .. 4c + 3 of every kQ-th of those partitions, kB
+// loads in flight per batch (one batch covers kQ * kB partitions), keeping
+// its own running state; the kQ lane groups are then combined, so every
+// lane c of the wave returns dims 4c .. 4c + 3 of the wave's state.
+template <uint32_t kD, uint32_t kB = 8>
+__device__ __forceinline__ MergeState merge_partitions(const DecodeArgs& a, uint64_t s0, uint32_t n, uint32_t first,
+                                                       uint32_t stride) {
+  constexpr uint32_t kL = kD / 4;   // lanes per partial row (16 bytes each)
+  constexpr uint32_t kQ = 64 / kL;  // partitions per load instruction
+  const uint32_t lane = threadIdx.x & 63U;
+  const uint32_t c = lane % kL, q = lane / kL;
+  const uint64_t ss = a.query_heads;
+  const float* os = a.ws_o + s0 * kD + 4 * c;
+  const float* ml = a.ws_ml + s0 * 2;
+  const uint32_t mine = n > first ? (n - first + stride - 1) / stride : 0U;  // this wave's partitions
+  MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  for (uint32_t b0 = 0; b0 < mine; b0 += kQ * kB) {
+    f32x4 ov[kB];
+    float2 pm[kB];
+#pragma unroll
+    for (uint32_t i = 0; i < kB; ++i) {
+      const uint32_t k = b0 + q + kQ * i;
+      const uint64_t at = static_cast<uint64_t>(k < mine ? first + k * stride : first) * ss;  // past the end: re-read
+      ov[i] = *reinterpret_cast<const f32x4*>(os + at * kD);
+      pm[i] = *reinterpret_cast<const float2*>(ml + at * 2);
+    }
+    float mb = st.m;
+#pragma unroll
+    for (uint32_t i = 0; i < kB; ++i) {
+      if (b0 + q + kQ * i >= mine) pm[i] = make_float2(-INFINITY, 0.0f);
+      mb = fmaxf(mb, pm[i].x);
+    }
+    const float r = isfinite(st.m) ? exp2f(st.m - mb) : 0.0f;
+    st.l *= r;
+    st.o *= r;
+    st.m = mb;
+#pragma unroll
+    for (uint32_t i = 0; i < kB; ++i) {
+      const float f = isfinite(pm[i].x) ? exp2f(pm[i].x - st.m) : 0.0f;
+      st.l = fmaf(pm[i].y, f, st.l);
+      st.o += ov[i] * f;
+    }
+  }
+#pragma unroll
+  for (uint32_t off = kL; off < 64; off <<= 1) {
+    MergeState other;
+    other.m = __shfl_xor(st.m, off, 64);
+    other.l = __shfl_xor(st.l, off, 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) other.o[j] = __shfl_xor(st.o[j], off, 64);
+    st = merge_combine(st, other);
+  }
+  return st;
+}
+
+// Writes a merged row: output dims 4c .. 4c + 3 from lanes c < Dv / 4 of
+// the calling wave, and the LSE (natural log) from lane 0.
+template <typename QE, uint32_t kD>
+__device__ __forceinline__ void merge_store_row(const DecodeArgs& a, uint64_t row, const MergeState& st) {
+  const uint32_t lane = threadIdx.x & 63U;
+  if (lane < kD / 4) {
+    const float inv = 1.0f / st.l;
+    if constexpr (std::is_same<QE, F32Elem>::value) {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + row * kD + 4 * lane) = st.o * inv;
+    } else {
+      const uint32_t w0 = QE::from_f(st.o[0] * inv) | (static_cast<uint32_t>(QE::from_f(st.o[1] * inv)) << 16);
+      const uint32_t w1 = QE::from_f(st.o[2] * inv) | (static_cast<uint32_t>(QE::from_f(st.o[3] * inv)) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.output) + row * kD + 4 * lane) = make_uint2(w0, w1);
+    }
+  }
+  if (lane == 0 && a.lse != nullptr) a.lse[row] = (st.m + log2f(st.l)) * kLn2;
 }
 
 
@@ -2027,7 +2133,7 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
       if (a.lse != nullptr && d == 0) a.lse[row] = (M + log2f(L)) * kLn2;
     } else {
       const uint64_t state = state_of(a, row, part);
-      put_partial<QE>(a, state * kD + d, O, 1.0f / L);
+      put_partial(a, state * kD + d, O);
       if (d == 0) {
         a.ws_ml[state * 2] = M;
         a.ws_ml[state * 2 + 1] = L;
@@ -2209,6 +2315,8 @@ __device__ __forceinline__ WorkItem direct_item(const DecodeArgs& a, uint32_t bi
 #pragma unroll
   for (int i = 0; i < kN; ++i) at[i] = min(min(p0 + i * kStep, t_end) >> a.block_shift, a.max_blocks - 1U);
   item.len = static_cast<uint32_t>(lens[item.seq]);  // first: its address needs nothing loaded
+  item.len = static_cast<uint32_t>(min(static_cast<uint64_t>(item.len),
+                                       static_cast<uint64_t>(a.parts) * a.partition_tokens));
 #pragma unroll
   for (int i = 0; i < kN; ++i) first[i] = static_cast<uint32_t>(row[at[i]]);
   if (p0 >= item.len) return item;
@@ -2296,35 +2404,39 @@ void decode_stream_heads_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K merge for at most kMergeRowParts partitions (the log-sum-exp
-// identity of paged_decode_attention.cu:780-852): one wave per (sequence,
-// query head) row, four rows per workgroup, no barriers. Only the
-// ceil(len / partition_tokens) partitions that hold tokens are read. Every
-// load of the row (m, l of lane p; two output dims of all partitions per
-// lane) is issued before any result is needed, so a row costs one memory
-// round trip; factors 2^(m_p - M) are broadcast with readlane.
+// Split-K merge kernels (the log-sum-exp identity of
+// paged_decode_attention.cu:780-852), launched after the decode kernel when
+// the decode launch does not merge its own partitions. Only the
+// min(ceil(len / partition_tokens), parts) partitions that hold tokens are
+// read. Partial outputs are F32 sums O_p weighted by f_p = 2^(m_p - M).
 // ---------------------------------------------------------------------------
 constexpr uint32_t kMergeThreads = 256;
 constexpr uint32_t kMergeRowsPerGroup = kMergeThreads / 64;
 constexpr uint32_t kMergeRowParts = 32;  // largest kParts instantiated
 
+__device__ __forceinline__ uint32_t merge_parts(const DecodeArgs& a, uint32_t seq) {
+  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
+  return static_cast<uint32_t>(min((static_cast<uint64_t>(len) + a.partition_tokens - 1) / a.partition_tokens,
+                                   static_cast<uint64_t>(a.parts)));
+}
+
+// At most kParts partitions, any value head size: one wave per (sequence,
+// query head) row, four rows per workgroup, no barriers. Every load of the
+// row (m, l of lane p; two output dims of all partitions per lane) is issued
+// before any result is needed, so a row costs one memory round trip; the
+// factors f_p are broadcast with readlane.
 template <typename QE, uint32_t kParts>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint32_t rows) {
   using QT = typename QE::T;
   const uint32_t lane = threadIdx.x & 63U;
   const uint32_t row = blockIdx.x * kMergeRowsPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint32_t seq = row / a.query_heads;
-  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
-  const uint32_t n = min(min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts), kParts);
-  // partition j of this row is state state_of(a, row, 0) + j * query_heads
+  const uint32_t n = min(merge_parts(a, row / a.query_heads), kParts);
   const uint64_t s0 = state_of(a, row, 0);
   const uint64_t sstride = a.query_heads;
   const float* ml = a.ws_ml + s0 * 2;
-  using PT = typename PartialOut<QE>::T;
   const uint32_t Dv = a.value_head_size;
-  const uint32_t ps = partial_stride<QE>(Dv);
-  const PT* os = static_cast<const PT*>(a.ws_o) + s0 * ps;
+  const float* os = a.ws_o + s0 * Dv;
   QT* out = static_cast<QT*>(a.output) + static_cast<uint64_t>(row) * Dv;
 
   const float mp = lane < n ? ml[2 * sstride * lane] : -INFINITY;
@@ -2334,28 +2446,18 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
     float v0[kParts], v1[kParts];
 #pragma unroll
     for (uint32_t j = 0; j < kParts; ++j) {
-      const PT* src = os + static_cast<uint64_t>(j) * sstride * ps + d;
-      if constexpr (PartialOut<QE>::kNormalised) {
-        // Both dims in one aligned 4-byte word (the row stride is even; the
-        // padding element past an odd Dv is never used).
-        const uint32_t w = j < n && d < Dv ? *reinterpret_cast<const uint32_t*>(src) : 0U;
-        v0[j] = QE::to_f(static_cast<uint16_t>(w & 0xFFFFU));
-        v1[j] = QE::to_f(static_cast<uint16_t>(w >> 16));
-      } else {
-        v0[j] = j < n && d < Dv ? src[0] : 0.0f;
-        v1[j] = j < n && d + 1 < Dv ? src[1] : 0.0f;
-      }
+      const float* src = os + static_cast<uint64_t>(j) * sstride * Dv + d;
+      v0[j] = j < n && d < Dv ? src[0] : 0.0f;
+      v1[j] = j < n && d + 1 < Dv ? src[1] : 0.0f;
     }
     const float M = wave_max_dpp(mp);
     // A partition without tokens would hold m = -inf and contributes nothing.
     const float f = isfinite(mp) ? exp2f(mp - M) : 0.0f;
     const float L = wave_sum_dpp(lp * f);
-    // Weight of partition p's stored output: f_p for sums, f_p l_p for normalised outputs.
-    const float wgt = PartialOut<QE>::kNormalised ? f * lp : f;
     float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
     for (uint32_t j = 0; j < kParts; ++j) {
-      const float fj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j));
+      const float fj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), j));
       o0 = fmaf(v0[j], fj, o0);
       o1 = fmaf(v1[j], fj, o1);
     }
@@ -2366,14 +2468,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a, uint
   }
 }
 
-// ---------------------------------------------------------------------------
-// Split-K merge for many partitions: one workgroup of 256 threads per
-// (sequence, query head) row.
-// Only the ceil(len / partition_tokens) partitions that hold tokens are read.
-// Factors f_p = 2^(m_p - M) go to LDS; then wave w accumulates partitions
-// p = w mod 4 for 2 dims per lane (unrolled for loads in flight), and the
-// four partial sums are added in LDS.
-// ---------------------------------------------------------------------------
+// Many partitions, any value head size: one workgroup of 256 threads per
+// row. Factors f_p go to LDS; then wave w accumulates partitions p = w mod 4
+// for 2 dims per lane (unrolled for loads in flight), and the four partial
+// sums are added in LDS.
 constexpr uint32_t kMergeWaves = kMergeThreads / 64;
 constexpr uint32_t kMergeWindow = 2048;
 constexpr uint32_t kMergeDimsPerPass = 128;
@@ -2385,17 +2483,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   __shared__ float red[kMergeWaves];
   __shared__ float part[kMergeWaves][kMergeDimsPerPass];
   const uint32_t row = blockIdx.x;
-  const uint32_t seq = row / a.query_heads;
-  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
-  const uint32_t n = (len + a.partition_tokens - 1) / a.partition_tokens;
-  // partition p of this row is state state_of(a, row, 0) + p * query_heads
+  const uint32_t n = merge_parts(a, row / a.query_heads);
   const uint64_t s0 = state_of(a, row, 0);
   const uint64_t sstride = a.query_heads;
   const float* ml = a.ws_ml + s0 * 2;
-  using PT = typename PartialOut<QE>::T;
-  const uint32_t ps = partial_stride<QE>(a.value_head_size);
-  const uint64_t pstride = sstride * ps;  // elements between partitions' partial outputs
-  const PT* os = static_cast<const PT*>(a.ws_o) + s0 * ps;
+  const uint32_t Dv = a.value_head_size;
+  const uint64_t pstride = sstride * Dv;  // elements between partitions' partial outputs
+  const float* os = a.ws_o + s0 * Dv;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63U;
   const uint32_t wave = tid >> 6;
@@ -2423,37 +2517,24 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   for (uint32_t w = 0; w < kMergeWaves; ++w) L += red[w];
   const float inv = 1.0f / L;
 
-  const uint32_t Dv = a.value_head_size;
   for (uint32_t d0 = 0; d0 < Dv; d0 += kMergeDimsPerPass) {
-    // F32 partials: dims lane and 64 + lane; 16-bit partials: the pair 2 lane,
-    // 2 lane + 1, read as one aligned 4-byte word.
-    const uint32_t d_a = PartialOut<QE>::kNormalised ? d0 + 2 * lane : d0 + lane;
-    const uint32_t d_b = PartialOut<QE>::kNormalised ? d_a + 1 : d0 + 64 + lane;
-    auto pair = [&](const PT* o, float& va, float& vb) {
-      if constexpr (PartialOut<QE>::kNormalised) {
-        const uint32_t w = d_a < Dv ? *reinterpret_cast<const uint32_t*>(o + d_a) : 0U;
-        va = QE::to_f(static_cast<uint16_t>(w & 0xFFFFU));
-        vb = QE::to_f(static_cast<uint16_t>(w >> 16));
-      } else {
-        va = d_a < Dv ? o[d_a] : 0.0f;
-        vb = d_b < Dv ? o[d_b] : 0.0f;
-      }
+    const uint32_t d_a = d0 + lane, d_b = d0 + 64 + lane;
+    auto pair = [&](const float* o, float& va, float& vb) {
+      va = d_a < Dv ? o[d_a] : 0.0f;
+      vb = d_b < Dv ? o[d_b] : 0.0f;
     };
     float acc_a = 0.0f, acc_b = 0.0f;
     for (uint32_t w0 = 0; w0 < n; w0 += kMergeWindow) {
       const uint32_t wn = min(kMergeWindow, n - w0);
       __syncthreads();
-      for (uint32_t p = tid; p < wn; p += kMergeThreads) {
-        const float f = exp2f(ml[2 * sstride * (w0 + p)] - M);
-        factor[p] = PartialOut<QE>::kNormalised ? f * ml[2 * sstride * (w0 + p) + 1] : f;  // weight of the stored output
-      }
+      for (uint32_t p = tid; p < wn; p += kMergeThreads) factor[p] = exp2f(ml[2 * sstride * (w0 + p)] - M);
       __syncthreads();
       uint32_t p = wave;
       for (; p + 3 * kMergeWaves < wn; p += 4 * kMergeWaves) {
-        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * pstride;
-        const PT* o1 = o0 + kMergeWaves * pstride;
-        const PT* o2 = o1 + kMergeWaves * pstride;
-        const PT* o3 = o2 + kMergeWaves * pstride;
+        const float* o0 = os + static_cast<uint64_t>(w0 + p) * pstride;
+        const float* o1 = o0 + kMergeWaves * pstride;
+        const float* o2 = o1 + kMergeWaves * pstride;
+        const float* o3 = o2 + kMergeWaves * pstride;
         float a0, b0, a1, b1, a2, b2, a3, b3;
         pair(o0, a0, b0);
         pair(o1, a1, b1);
@@ -2471,7 +2552,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
         acc_b = fmaf(b3, f3, acc_b);
       }
       for (; p < wn; p += kMergeWaves) {
-        const PT* o0 = os + static_cast<uint64_t>(w0 + p) * pstride;
+        const float* o0 = os + static_cast<uint64_t>(w0 + p) * pstride;
         float a0, b0;
         pair(o0, a0, b0);
         acc_a = fmaf(a0, factor[p], acc_a);
@@ -2492,92 +2573,43 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(DecodeArgs a)
   if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
 }
 
-// Split-K merge, latency path for the common shape: 16-bit partials, Dv = 128,
-// at most 256 partitions (partial rows of 256 bytes, 16-byte aligned). One
-// workgroup of 256 threads per row, merging in two stages of the log-sum-exp
-// identity. Thread (g, c) owns dims 8c..8c+7 of the partitions of group g
-// (partitions g, g + 16, ...). All of a row's partial and (m, l) loads are
-// issued at the start, so the row costs one memory round trip.
-//   Stage 1 (registers): each group's state (M_g, L_g, O_g) from its own
-//     maximum, M_g = max m_p, L_g = sum 2^(m_p - M_g) l_p, O_g = sum
-//     2^(m_p - M_g) l_p o_p (o_p is the stored O_p / l_p).
-//   Stage 2 (LDS, one barrier): M = max M_g, L = sum 2^(M_g - M) L_g,
-//     out = sum 2^(M_g - M) O_g / L.
-// A group without partitions has M_g = -inf and weight 0.
-constexpr uint32_t kMergeFastParts = 256;
-constexpr uint32_t kMergeFastDim = 128;
-
-template <typename QE>
-__global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs a) {
-  using QT = typename QE::T;
-  constexpr uint32_t kGroups = kMergeThreads / 16;            // partition groups
-  constexpr uint32_t kPerThread = kMergeFastParts / kGroups;  // partitions per thread
-  __shared__ float part[kGroups][kMergeFastDim + 4];
-  __shared__ float group_ml[kGroups][2];
-  const uint32_t row = blockIdx.x;
-  const uint32_t seq = row / a.query_heads;
-  const uint32_t len = static_cast<uint32_t>(a.sequence_lengths[seq]);
-  const uint32_t n = min((len + a.partition_tokens - 1) / a.partition_tokens, a.parts);  // <= 256
-  // partition p of this row is state state_of(a, row, 0) + p * query_heads
-  const uint64_t s0 = state_of(a, row, 0);
-  const uint64_t sstride = a.query_heads;
-  const float* ml = a.ws_ml + s0 * 2;
-  const uint16_t* os = static_cast<const uint16_t*>(a.ws_o) + s0 * kMergeFastDim;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t c = tid & 15U;
-  const uint32_t g = tid >> 4;
-
-  uint4 ov[kPerThread];
-  float mp[kPerThread], lp[kPerThread];
-#pragma unroll
-  for (uint32_t i = 0; i < kPerThread; ++i) {
-    const uint32_t p = g + kGroups * i;
-    const bool live = p < n;
-    ov[i] = live ? *reinterpret_cast<const uint4*>(os + static_cast<uint64_t>(p) * sstride * kMergeFastDim + 8 * c)
-                 : make_uint4(0U, 0U, 0U, 0U);
-    mp[i] = live ? ml[2 * sstride * p] : -INFINITY;
-    lp[i] = live ? ml[2 * sstride * p + 1] : 0.0f;
-  }
-
-  // Stage 1: this group's partitions.
-  float Mg = -INFINITY;
-#pragma unroll
-  for (uint32_t i = 0; i < kPerThread; ++i) Mg = fmaxf(Mg, mp[i]);
-  float Lg = 0.0f;
-  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (uint32_t i = 0; i < kPerThread; ++i) {
-    const float f = g + kGroups * i < n ? exp2f(mp[i] - Mg) * lp[i] : 0.0f;  // weight of the stored O_p / l_p
-    Lg += f;
-    const uint32_t words[4] = {ov[i].x, ov[i].y, ov[i].z, ov[i].w};
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-      acc[2 * j] = fmaf(QE::to_f(static_cast<uint16_t>(words[j] & 0xFFFFU)), f, acc[2 * j]);
-      acc[2 * j + 1] = fmaf(QE::to_f(static_cast<uint16_t>(words[j] >> 16)), f, acc[2 * j + 1]);
+// Value head size 64, 128 or 256 with 16-byte aligned partial rows, any
+// partition count: kW waves per row, each loading 16-byte pieces of its
+// partitions (w, w + kW, ...) in batches of kB per lane. With kW = 1 a
+// workgroup holds four independent rows; otherwise one row, merged in two
+// stages of the log-sum-exp identity (the two-stage merge of long contexts):
+//   Stage 1 (registers, merge_partitions): each wave's own running state
+//     over its partitions, its lane groups then combined.
+//   Stage 2 (LDS, one barrier): wave 0 combines the kW wave states.
+// The launch picks kW and kB so that one batch covers the row's partitions.
+template <typename QE, uint32_t kD, uint32_t kW, uint32_t kB>
+__global__ __launch_bounds__(kW == 1 ? 256 : kW * 64) void merge_rows_kernel(DecodeArgs a, uint32_t rows) {
+  constexpr uint32_t kRowsPerGroup = kW == 1 ? 4 : 1;
+  __shared__ float wave_ml[kW][2];
+  __shared__ f32x4 wave_o[kW][kD / 4];
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63U;
+  const uint32_t row = kW == 1 ? blockIdx.x * kRowsPerGroup + wave : blockIdx.x;
+  if (row >= rows) return;  // kW == 1 only: whole workgroups otherwise
+  const uint32_t n = merge_parts(a, row / a.query_heads);
+  const uint32_t w = kW == 1 ? 0U : wave;
+  const MergeState st = merge_partitions<kD, kB>(a, state_of(a, row, 0), n, w, kW);
+  if constexpr (kW == 1) {
+    merge_store_row<QE, kD>(a, row, st);
+  } else {
+    if (lane < kD / 4) wave_o[wave][lane] = st.o;
+    if (lane == 0) {
+      wave_ml[wave][0] = st.m;
+      wave_ml[wave][1] = st.l;
     }
-  }
+    __syncthreads();
+    if (wave != 0) return;
+    MergeState total = st;
 #pragma unroll
-  for (uint32_t j = 0; j < 8; ++j) part[g][8 * c + j] = acc[j];
-  if (c == 0) {
-    group_ml[g][0] = Mg;
-    group_ml[g][1] = Lg;
-  }
-  __syncthreads();
-
-  // Stage 2: the group states.
-  float M = -INFINITY;
-#pragma unroll
-  for (uint32_t v = 0; v < kGroups; ++v) M = fmaxf(M, group_ml[v][0]);
-  if (tid < kMergeFastDim) {
-    float O = 0.0f, L = 0.0f;
-#pragma unroll
-    for (uint32_t v = 0; v < kGroups; ++v) {
-      const float f = isfinite(group_ml[v][0]) ? exp2f(group_ml[v][0] - M) : 0.0f;
-      L = fmaf(group_ml[v][1], f, L);
-      O = fmaf(part[v][tid], f, O);
-    }
-    static_cast<QT*>(a.output)[static_cast<uint64_t>(row) * kMergeFastDim + tid] = QE::from_f(O / L);
-    if (tid == 0 && a.lse != nullptr) a.lse[row] = (M + log2f(L)) * kLn2;
+    for (uint32_t v = 1; v < kW; ++v)
+      total = merge_combine(total, MergeState{wave_ml[v][0], wave_ml[v][1],
+                                              lane < kD / 4 ? wave_o[v][lane] : f32x4{0.0f, 0.0f, 0.0f, 0.0f}});
+    merge_store_row<QE, kD>(a, row, total);
   }
 }
 
@@ -2586,6 +2618,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows128_kernel(DecodeArgs
 // ---------------------------------------------------------------------------
 thread_local std::string g_last_error;
 thread_local const char* g_last_family = "";
+thread_local const char* g_last_kernel = "";  // decode kernel of the last successful call
+thread_local const char* g_launch_kernel = "";  // decode kernel of the launch in progress
 thread_local uint32_t g_last_internal_split = 0;
 std::atomic<uint64_t> g_decode_launches{0};
 std::atomic<uint64_t> g_rope_launches{0};
@@ -2798,11 +2832,16 @@ int validate(const Problem& p) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
 
-// The matrix-core kernels store the output (and 16-bit partial states) four
-// 16-bit elements at a time with 8-byte stores.
+// The matrix-core kernels store the output four 16-bit elements at a time
+// with 8-byte stores, (m, l) pairs as 8 bytes and partial rows four F32
+// elements at a time with 16-byte stores.
 bool stores_aligned8(const Problem& p) {
   const auto a8 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7U) == 0; };
-  return a8(p.output) && (p.workspace == nullptr || a8(p.workspace));
+  if (!a8(p.output)) return false;
+  const uint64_t parts = parts_for(p.max_sequence_length, p.partition_tokens);
+  if (parts == 1 || p.workspace == nullptr) return true;
+  const float* ws_o = p.workspace + static_cast<uint64_t>(p.sequences) * p.query_heads * parts * 2;
+  return a8(p.workspace) && aligned16(ws_o);
 }
 
 // Shape-level eligibility of the matrix-core kernel.
@@ -2829,19 +2868,47 @@ uint32_t log2u(uint32_t v) {
   return r;
 }
 
+// Launches merge_rows_kernel with kW waves per row (four rows per workgroup
+// at kW = 1) and kB loads per lane: the smallest shape whose one batch
+// covers `parts` partitions (kQ = 256 / kD partitions per load), else 8
+// waves of 8-load batches.
+template <typename QE, uint32_t kD>
+void launch_merge_rows(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
+  constexpr uint32_t kQ = 256 / kD;
+  const uint32_t parts = args.parts;
+  const dim3 quad((rows + 3) / 4), one(rows);
+  if (parts <= kQ * 2) {
+    hipLaunchKernelGGL((merge_rows_kernel<QE, kD, 1, 2>), quad, dim3(256), 0, stream, args, rows);
+  } else if (parts <= kQ * 4) {
+    hipLaunchKernelGGL((merge_rows_kernel<QE, kD, 1, 4>), quad, dim3(256), 0, stream, args, rows);
+  } else if (parts <= kQ * 8) {
+    hipLaunchKernelGGL((merge_rows_kernel<QE, kD, 1, 8>), quad, dim3(256), 0, stream, args, rows);
+  } else if (parts <= kQ * 8 * 4) {
+    hipLaunchKernelGGL((merge_rows_kernel<QE, kD, 4, 8>), one, dim3(256), 0, stream, args, rows);
+  } else {
+    hipLaunchKernelGGL((merge_rows_kernel<QE, kD, 8, 8>), one, dim3(512), 0, stream, args, rows);
+  }
+}
+
 template <typename QE>
 int launch_merge(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_MERGE, stream);
   const dim3 grid((rows + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup);
-  if (args.parts <= 8) {
+  const uint32_t dv = args.value_head_size;
+  const bool rows_aligned = reinterpret_cast<uintptr_t>(args.ws_o) % 16 == 0 &&
+                            reinterpret_cast<uintptr_t>(args.ws_ml) % 8 == 0;
+  if (rows_aligned && dv == 64) {
+    launch_merge_rows<QE, 64>(args, rows, stream);
+  } else if (rows_aligned && dv == 128) {
+    launch_merge_rows<QE, 128>(args, rows, stream);
+  } else if (rows_aligned && dv == 256) {
+    launch_merge_rows<QE, 256>(args, rows, stream);
+  } else if (args.parts <= 8) {
     hipLaunchKernelGGL((merge_kernel<QE, 8>), grid, dim3(kMergeThreads), 0, stream, args, rows);
   } else if (args.parts <= 16) {
     hipLaunchKernelGGL((merge_kernel<QE, 16>), grid, dim3(kMergeThreads), 0, stream, args, rows);
   } else if (args.parts <= kMergeRowParts) {
     hipLaunchKernelGGL((merge_kernel<QE, kMergeRowParts>), grid, dim3(kMergeThreads), 0, stream, args, rows);
-  } else if (PartialOut<QE>::kNormalised && args.value_head_size == kMergeFastDim &&
-             args.parts <= kMergeFastParts && reinterpret_cast<uintptr_t>(args.ws_o) % 16 == 0) {
-    hipLaunchKernelGGL(merge_rows128_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
   } else {
     hipLaunchKernelGGL(merge_wide_kernel<QE>, dim3(rows), dim3(kMergeThreads), 0, stream, args);
   }
@@ -2851,6 +2918,7 @@ int launch_merge(const DecodeArgs& args, uint32_t rows, hipStream_t stream) {
 template <typename QE, bool kFp8, int kHT, int kWaves>
 int launch_mfma(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  g_launch_kernel = "decode_mfma_kernel";
   hipLaunchKernelGGL((decode_mfma_kernel<QE, kFp8, kHT, kWaves>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kWaves * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
@@ -2868,6 +2936,7 @@ template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup,
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   const uint64_t groups = (items + kGroup - 1) / kGroup;
+  g_launch_kernel = "decode_stream_group_kernel";
   hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, kDirect>), dim3(static_cast<uint32_t>(groups)),
                      dim3(kGroup * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
@@ -2876,6 +2945,7 @@ int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stre
 template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim, int kNt = -1>
 int launch_stream(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  g_launch_kernel = "decode_stream_kernel";
   hipLaunchKernelGGL((decode_stream_kernel<QE, kFp8, kSplit, kHT, kD, kNt>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kSplit * 64), 0, stream, args);
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
@@ -2968,6 +3038,7 @@ int launch_stream_heads(const DecodeArgs& args, uint64_t items, uint32_t group, 
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   static_assert(4 * Dec::kWaveBytes <= 64 * 1024, "four waves' stages fit in 64 KiB of LDS");
   const dim3 grid(static_cast<uint32_t>(items));
+  g_launch_kernel = "decode_stream_heads_kernel";
   if (group <= 64) {
     hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 2, kD>), grid, dim3(128), 0, stream, args);
   } else if (group <= 96) {
@@ -2998,6 +3069,7 @@ bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
 
 template <typename QE, typename CE, bool kVecK, uint32_t kDvl, bool kQLds, uint32_t kH>
 int launch_vector_kernel(const DecodeArgs& args, uint64_t grid, hipStream_t stream) {
+  g_launch_kernel = "decode_vector_kernel";
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   hipLaunchKernelGGL((decode_vector_kernel<QE, CE, kVecK, kDvl, kQLds, kH>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kVecThreads), 0, stream, args);
@@ -3089,6 +3161,7 @@ int run_typed(const Problem& p, hipStream_t stream) {
   args.parts = static_cast<uint32_t>(parts);
   args.scale_stride = p.scale_stride;
   args.score_scale_log2 = p.scale * kLog2e;
+  g_launch_kernel = "";
 
   int status = LOOM_HIP_SUCCESS;
   bool use_narrow = false, use_mfma = false, use_heads = false;
@@ -3415,6 +3488,7 @@ int run(Problem p, void* stream) {
   }
   if (status == LOOM_HIP_SUCCESS) {
     g_last_internal_split = internal;
+    g_last_kernel = g_launch_kernel;
     g_decode_launches.fetch_add(1, std::memory_order_relaxed);
   }
   return status;
@@ -3607,6 +3681,8 @@ const char* loom_hip_last_error_message(void) { return g_last_error.c_str(); }
 const char* loom_hip_last_kernel_family(void) { return g_last_family; }
 
 uint32_t loom_hip_last_internal_partition_tokens(void) { return g_last_internal_split; }
+
+const char* loom_hip_last_kernel_name(void) { return g_last_kernel; }
 
 int loom_hip_launch_count(uint32_t operation, uint64_t* count) {
   if ((operation != LOOM_HIP_PAGED_DECODE_ATTENTION && operation != LOOM_HIP_ROPE_PAGED_KV_WRITE) ||
@@ -3944,3 +4020,4 @@ extern "C" int loom_hip_wave_trace_stall_read(void* host, uint64_t bytes) {
   return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_wave_stall), n, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
 }
 #endif
+

@@ -13,9 +13,11 @@ This tool compiles ``paged_decode_attention.hip`` to gfx950 assembly and
 scans every kernel. For each load that stands inside an inline-asm region and
 returns into registers (scalar ``s_load_dword*`` / ``s_buffer_load_dword*``,
 vector ``global_load_dword*`` / ``buffer_load_dword*`` without the LDS
-variant), it reports any later instruction that names a destination register
-before the next wait on that load's counter (``lgkmcnt`` for scalar loads,
-``vmcnt`` for vector loads).
+variant), it reports any instruction on a path from the load (through
+branches and loop back-edges) that names a destination register before a
+wait that completes the load: ``lgkmcnt(0)`` for scalar loads, which may
+return out of order, and ``vmcnt(N)`` with at least N vector loads issued
+after it for vector loads, which return in order.
 
 Usage: ``python -m attnarc_amd.isa_check`` (about 2.5 minutes of compile),
 or ``python -m attnarc_amd.isa_check FILE.s`` to scan assembly already made.
@@ -55,9 +57,40 @@ def _named(text: str, kind: str) -> set[int]:
     return regs
 
 
+_VM_LOAD = re.compile(r"\s*(global_load\w*|buffer_load\w*|flat_load\w*)\b")
+_WAIT = re.compile(r"\s*s_waitcnt\b(.*)")
+_BRANCH = re.compile(r"\s*(s_branch|s_cbranch_\w+)\s+(\S+)")
+_LABEL = re.compile(r"^(\.?[A-Za-z_][\w.$]*):")
+
+
+def _wait_count(args: str, counter: str) -> int | None:
+    """The N of ``counter(N)`` in an s_waitcnt's operands, or None."""
+    m = re.search(counter + r"\((\d+)\)", args)
+    return int(m.group(1)) if m else None
+
+
+def _covers(kind: str, n: int, loads_after: int) -> bool:
+    """Whether a wait for counter value n completes the load. Vector loads
+    return in issue order, so vmcnt(n) completes every load with at least n
+    loads issued after it; scalar loads may return out of order, so only
+    lgkmcnt(0) completes a given one."""
+    return n == 0 if kind == "s" else loads_after >= n
+
+
 def scan(asm: str, window: int = 600) -> list[str]:
-    """Hazards in ``asm`` (AMDGPU assembly text), one line of text each."""
+    """Hazards in ``asm`` (AMDGPU assembly text), one line of text each.
+
+    From each inline-asm load into registers, every path is followed
+    (branches to labels, taken and not taken, loop back-edges included) up to
+    ``window`` instructions, counting the vector loads issued after it, until
+    a wait completes the load; an instruction on the way that names a
+    destination register is a hazard."""
     lines = asm.split("\n")
+    labels = {}
+    for i, line in enumerate(lines):
+        m = _LABEL.match(line)
+        if m:
+            labels[m.group(1)] = i
     found: list[str] = []
     func = None
     in_asm = False
@@ -79,14 +112,83 @@ def scan(asm: str, window: int = 600) -> list[str]:
             kind, counter, dest = "v", "vmcnt", _reg_set(mv.group(2), "v")
         else:
             continue
-        for j in range(i + 1, min(i + window, len(lines))):
-            later = lines[j].split(";")[0]
-            if "s_waitcnt" in later and counter in later:
-                break
-            if _named(later, kind) & dest:
-                found.append(f"{func}: line {i + 1}: {code.strip()} -> line {j + 1}: {later.strip()}")
-                break
+        hit = _follow(lines, labels, i + 1, kind, counter, dest, window)
+        if hit is not None:
+            found.append(f"{func}: line {i + 1}: {code.strip()} -> line {hit + 1}: {lines[hit].split(';')[0].strip()}")
     return found
+
+
+_ANDN2_VCC = re.compile(r"\s*s_andn2_b64\s+vcc,\s*exec,\s*(s\[\d+:\d+\])")
+
+
+def _never_taken(lines, j) -> bool:
+    """A branch the compiler emits with a constant condition: ``s_cbranch_vccnz``
+    right after ``vcc = exec & ~s[a:b]`` where s[a:b] was last set to -1 in
+    code reachable only by falling through from there (no label between:
+    vcc = 0). The compiler writes this for a loop exit whose other side is
+    decided elsewhere."""
+    code = lines[j].split(";")[0]
+    if "s_cbranch_vccnz" not in code:
+        return False
+    k = j - 1
+    while k >= 0 and not lines[k].split(";")[0].strip():
+        k -= 1
+    m = _ANDN2_VCC.match(lines[k].split(";")[0]) if k >= 0 else None
+    if not m:
+        # one scalar move may sit between the two
+        k -= 1
+        m = _ANDN2_VCC.match(lines[k].split(";")[0]) if k >= 0 else None
+        if not m:
+            return False
+    reg = m.group(1)
+    for i in range(k - 1, max(-1, k - 200), -1):
+        c = lines[i].split(";")[0]
+        if _LABEL.match(lines[i]):  # a join: other paths may set the register
+            return False
+        if reg in c and re.match(r"\s*s_\w+\s+" + re.escape(reg) + r",", c):
+            return bool(re.match(r"\s*s_mov_b64\s+" + re.escape(reg) + r",\s*-1\s*$", c))
+    return False
+
+
+def _follow(lines, labels, start, kind, counter, dest, window):
+    """First line on any path from ``start`` that names a register of
+    ``dest`` before a wait completes the load, or None."""
+    best: dict[int, int] = {}  # line -> fewest loads-after seen there (revisit only with fewer)
+    stack = [(start, 0, 0)]  # (line, loads issued after the load, instructions walked)
+    while stack:
+        j, after, steps = stack.pop()
+        while j < len(lines) and steps < window:
+            if j in best and best[j] <= after:
+                break
+            best[j] = after
+            line = lines[j]
+            if _FUNC.match(line) or ".Lfunc_end" in line:
+                break
+            code = line.split(";")[0]
+            if not code.strip() or _LABEL.match(line):
+                j += 1
+                continue
+            steps += 1
+            w = _WAIT.match(code)
+            if w:
+                n = _wait_count(w.group(1), counter)
+                if n is not None and _covers(kind, n, after):
+                    break
+            if _named(code, kind) & dest:
+                return j
+            if _VM_LOAD.match(code):
+                after += 1
+            b = _BRANCH.match(code)
+            if b:
+                target = labels.get(b.group(2))
+                if target is not None and not _never_taken(lines, j):
+                    stack.append((target, after, steps))
+                if b.group(1) == "s_branch":
+                    break  # unconditional: only the target continues
+            if code.strip().startswith("s_endpgm"):
+                break
+            j += 1
+    return None
 
 
 def compile_asm(out_path: str) -> None:

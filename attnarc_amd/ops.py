@@ -67,6 +67,25 @@ def _views(*tensors: torch.Tensor):
     return views
 
 
+_I64 = (-(1 << 63), (1 << 63) - 1)
+_U32_MAX = (1 << 32) - 1
+
+
+def _abi_i64(value: int) -> bool:
+    """Whether ``value`` passes to an int64 ABI argument unchanged (ctypes
+    would wrap it silently otherwise)."""
+    return _I64[0] <= value <= _I64[1]
+
+
+def _abi_u32(value: int, what: str = "shape") -> int:
+    """``value`` for a uint32 ABI argument; anything outside [0, 2^32) is
+    refused with the contract's ABI message instead of wrapping."""
+    value = int(value)
+    if not 0 <= value <= _U32_MAX:
+        raise RuntimeError(f"Loom paged decode {what} exceeds the HIP ABI")
+    return value
+
+
 def _raise_unless_ok(status: int, operation: str) -> None:
     """A refused view set raises RuntimeError: the contract's message, or the bridge's."""
     if status == _native.VIEWS_OK:
@@ -94,6 +113,8 @@ def supports_paged_decode_attention(
     facts only Python sees (an ``int`` length, no autograd).
     """
     if isinstance(max_sequence_length, bool) or not isinstance(max_sequence_length, int):
+        return False
+    if not _abi_i64(max_sequence_length):  # the library's range check never sees a wrapped value
         return False
     if any(t.requires_grad for t in (query, key_cache, value_cache)):
         return False
@@ -132,6 +153,8 @@ def paged_decode_attention_out(
     lib = _native.lib()
     views = _views(query, key_cache, value_cache, block_tables, sequence_lengths, output)
     max_sequence_length = int(max_sequence_length)
+    if not _abi_i64(max_sequence_length):
+        raise RuntimeError("Loom paged decode shape exceeds the HIP ABI")
     elements = ctypes.c_uint64()
     _raise_unless_ok(
         lib.loom_hip_views_paged_decode_workspace_elements(views, max_sequence_length, float(scale),
@@ -277,7 +300,8 @@ def paged_decode_attention_extended(
     if scale is None:
         scale = query.shape[-1] ** -0.5
     sequences, query_heads, head_size = (int(x) for x in query.shape)
-    max_sequence_length = int(max_sequence_length)
+    max_sequence_length = _abi_u32(max_sequence_length)
+    partition_tokens = _abi_u32(partition_tokens, "partition size")
     if output is None:
         output = torch.empty((sequences, query_heads, dv), device=query.device, dtype=query.dtype)
     if lse is None and return_lse:
@@ -460,6 +484,11 @@ def last_internal_partition_tokens() -> int:
     """Partition size of the internal split of the last successful paged-decode
     call on this thread (0: it ran as the caller asked)."""
     return int(_native.lib().loom_hip_last_internal_partition_tokens())
+
+
+def last_kernel_name() -> str:
+    """Decode kernel the last successful paged-decode call on this thread launched."""
+    return _native.lib().loom_hip_last_kernel_name().decode()
 
 
 def launch_count(operation: int = _native.PAGED_DECODE_ATTENTION) -> int:

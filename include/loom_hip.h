@@ -387,6 +387,15 @@ const char* loom_hip_last_kernel_family(void);
 uint32_t loom_hip_last_internal_partition_tokens(void);
 
 /*
+ * Name of the decode kernel that the last successful paged decode call on
+ * this thread launched ("decode_stream_group_kernel", "decode_stream_kernel",
+ * "decode_stream_heads_kernel", "decode_mfma_kernel" or
+ * "decode_vector_kernel"); "" before the first. No reference counterpart: a
+ * diagnostic for profiling (the kernel a rocprof trace names).
+ */
+const char* loom_hip_last_kernel_name(void);
+
+/*
  * Relaxed atomic launch counters (replace loom_cuda_bridge_launch_count /
  * _reset_launch_count, cuda/mod.rs:733-774). One successful decode call
  * counts once regardless of how many kernels it launches.

@@ -51,3 +51,48 @@ def test_vector_load_read_before_vmcnt_is_reported_and_lds_dma_is_not():
     waited = _asm("\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v2, s[0:1]", "\t;;#ASMEND",
                   "\ts_waitcnt vmcnt(0)", "\tv_mov_b32_e32 v20, v5")
     assert scan(waited) == []
+
+
+def test_partial_vmcnt_covers_only_with_enough_later_loads():
+    # vmcnt(1) with one later load completes the first load ...
+    covered = _asm("\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v2, s[0:1]", "\t;;#ASMEND",
+                   "\tglobal_load_dwordx4 v[8:11], v2, s[0:1] offset:16", "\ts_waitcnt vmcnt(1)",
+                   "\tv_mov_b32_e32 v20, v5")
+    assert scan(covered) == []
+    # ... but not with none: the load may still be in flight
+    uncovered = _asm("\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v2, s[0:1]", "\t;;#ASMEND",
+                     "\ts_waitcnt vmcnt(1)", "\tv_mov_b32_e32 v20, v5", "\ts_waitcnt vmcnt(0)")
+    assert len(scan(uncovered)) == 1
+
+
+def test_scalar_load_needs_lgkmcnt_zero():
+    asm = _asm("\t;;#ASMSTART", "\ts_load_dword s0, s[2:3], 0x0", "\t;;#ASMEND", "\ts_load_dword s9, s[2:3], 0x4",
+               "\ts_waitcnt lgkmcnt(1)", "\ts_add_u32 s4, s0, s6", "\ts_waitcnt lgkmcnt(0)")
+    assert len(scan(asm)) == 1
+
+
+def test_hazard_reached_through_a_loop_back_edge_is_reported():
+    # the use precedes the load in text order but follows it around the loop
+    asm = _asm(".LBB0_1:", "\tv_mov_b32_e32 v20, v5", "\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v2, s[0:1]",
+               "\t;;#ASMEND", "\ts_cbranch_scc1 .LBB0_1", "\ts_waitcnt vmcnt(0)", "\ts_endpgm")
+    found = scan(asm)
+    assert len(found) == 1 and "v_mov_b32_e32 v20, v5" in found[0]
+
+
+def test_both_sides_of_a_branch_are_followed():
+    asm = _asm("\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v2, s[0:1]", "\t;;#ASMEND",
+               "\ts_cbranch_scc0 .LBB0_2", "\ts_waitcnt vmcnt(0)", "\ts_branch .LBB0_3", ".LBB0_2:",
+               "\tv_add_f32_e32 v21, v6, v6", ".LBB0_3:", "\ts_endpgm")
+    found = scan(asm)
+    assert len(found) == 1 and "v_add_f32_e32 v21, v6, v6" in found[0]
+
+
+def test_constant_false_loop_branch_is_not_followed():
+    # vcc = exec & ~(-1) = 0: the s_cbranch_vccnz back to the header is never taken
+    asm = _asm(".LBB0_1:", "\tv_mov_b32_e32 v20, v5", "\t;;#ASMSTART", "\tglobal_load_dwordx4 v[4:7], v2, s[0:1]",
+               "\t;;#ASMEND", "\ts_mov_b64 s[8:9], -1", "\ts_cbranch_scc1 .LBB0_2", "\ts_andn2_b64 vcc, exec, s[8:9]",
+               "\ts_cbranch_vccnz .LBB0_1", ".LBB0_2:", "\ts_waitcnt vmcnt(0)", "\ts_endpgm")
+    assert scan(asm) == []
+    # with the register set elsewhere the branch may be taken
+    live = asm.replace("s_mov_b64 s[8:9], -1", "s_mov_b64 s[8:9], s[10:11]")
+    assert len(scan(live)) == 1
