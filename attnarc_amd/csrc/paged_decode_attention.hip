@@ -1770,6 +1770,12 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   const uint32_t pt = a.partition_tokens;
   it.kvh = bid % a.kv_heads;
   const uint32_t pair = bid / a.kv_heads;
+  // Odd (sequence, partition) pairs swap the halves of the KV heads: the
+  // dispatcher deals workgroups to the XCDs in turn, and with the head
+  // varying fastest each XCD would otherwise read the same half of every
+  // token row (the XCDs holding the second half finished up to 15 us later;
+  // C3 call 205.2 -> 204.8 us).
+  if ((a.kv_heads & 1U) == 0 && (pair & 1U)) it.kvh ^= a.kv_heads / 2;
   // Class 0: full partitions (len / pt per sequence); class 1: one partial
   // last partition per sequence whose length is not a multiple of pt.
   uint32_t before = 0;  // pairs of earlier classes and chunks
@@ -1795,6 +1801,51 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
         it.part = cls == 0 ? r - (__builtin_amdgcn_readlane(incl, src) - __builtin_amdgcn_readlane(n, src))
                            : __builtin_amdgcn_readlane(full, src);
         it.valid = true;
+        return it;
+      }
+      before += total;
+    }
+  }
+  return it;
+}
+
+// Schedule of the two-partition workgroups (decode_stream_group_kernel
+// with kPair): unit `unit` is (sequence, pair of partitions 2j and 2j + 1,
+// group of `heads` adjacent KV heads), numbered as schedule_item numbers its
+// items (every full pair first, then each sequence's last, shorter pair;
+// the head group varies fastest). Wave w of the workgroup takes KV head
+// w % heads of the group and partition 2j + w / heads. valid is false for a
+// partition past its sequence's end (only 2j + 1 can be); len is 0 for a
+// unit past the schedule's end (the grid is sized for the longest sequence).
+__device__ __forceinline__ WorkItem pair_item(const DecodeArgs& a, uint32_t unit, uint32_t heads, uint32_t wave) {
+  WorkItem it{0, 0, 0, 0, false};
+  const uint32_t lane = threadIdx.x & 63U;
+  const uint32_t pt2 = 2U * a.partition_tokens;
+  const uint32_t groups = a.kv_heads / heads;
+  const uint32_t hg = unit % groups;
+  const uint32_t pair = unit / groups;
+  uint32_t before = 0;
+#pragma unroll 1
+  for (int cls = 0; cls < 2; ++cls) {
+#pragma unroll 1
+    for (uint32_t c0 = 0; c0 < a.sequences; c0 += 64) {
+      const uint32_t len = static_cast<uint32_t>(min(static_cast<uint64_t>(lengths_chunk(a, c0, lane)),
+                                                     static_cast<uint64_t>(a.parts) * a.partition_tokens));
+      const uint32_t full = len / pt2;
+      const uint32_t n = cls == 0 ? full : (len % pt2 != 0 ? 1U : 0U);
+      const uint32_t incl = wave_inclusive_sum(n, lane);
+      const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
+      if (pair < before + total) {
+        const uint32_t r = pair - before;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(incl > r);
+        const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(hit));
+        const uint32_t j = cls == 0 ? r - (__builtin_amdgcn_readlane(incl, src) - __builtin_amdgcn_readlane(n, src))
+                                    : __builtin_amdgcn_readlane(full, src);
+        it.seq = c0 + src;
+        it.len = __builtin_amdgcn_readlane(len, src);
+        it.kvh = hg * heads + wave % heads;
+        it.part = 2U * j + wave / heads;
+        it.valid = it.part * a.partition_tokens < it.len;
         return it;
       }
       before += total;
@@ -1927,14 +1978,53 @@ __device__ __forceinline__ void merge_store_row(const DecodeArgs& a, uint64_t ro
 }
 
 
+// The state of a wave's item (head c of lane (g, c): maximum m, sum l, and
+// dims dt * 16 + 4g .. + 3 of O) in LDS at `tile`, lane by lane, for the
+// wave that merges it (pair_combine). An empty item publishes m = -inf,
+// l = 0.
+template <typename Dec>
+__device__ __forceinline__ void pair_publish(uint8_t* tile, float m, float l, const f32x4 (&acc)[Dec::kDt]) {
+  static_assert(Dec::kWaveBytes >= Dec::kDt * 1024 + 512, "the state fits the wave's stages");
+  const uint32_t lane = threadIdx.x & 63U;
+  f32x4* o = reinterpret_cast<f32x4*>(tile);
+#pragma unroll
+  for (int dt = 0; dt < Dec::kDt; ++dt) o[dt * 64 + lane] = acc[dt];  // lane-linear: no bank conflicts
+  reinterpret_cast<float2*>(tile + Dec::kDt * 1024)[lane] = make_float2(m, l);
+}
+
+template <typename Dec>
+__device__ __forceinline__ void pair_publish_empty(uint8_t* tile) {
+  f32x4 zero[Dec::kDt];
+#pragma unroll
+  for (int dt = 0; dt < Dec::kDt; ++dt) zero[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  pair_publish<Dec>(tile, -INFINITY, 0.0f, zero);
+}
+
+// Folds the partner's published state into this wave's (m, l, O) by the
+// log-sum-exp identity; this wave's item holds tokens, so m is finite.
+template <typename Dec>
+__device__ __forceinline__ void pair_combine(const uint8_t* tile, float& m, float& l, f32x4 (&acc)[Dec::kDt]) {
+  const uint32_t lane = threadIdx.x & 63U;
+  const float2 ml = reinterpret_cast<const float2*>(tile + Dec::kDt * 1024)[lane];
+  const float mn = fmaxf(m, ml.x);
+  const float fa = __builtin_amdgcn_exp2f(m - mn);
+  const float fb = isfinite(ml.x) ? __builtin_amdgcn_exp2f(ml.x - mn) : 0.0f;
+  const f32x4* o = reinterpret_cast<const f32x4*>(tile);
+#pragma unroll
+  for (int dt = 0; dt < Dec::kDt; ++dt) acc[dt] = acc[dt] * fa + o[dt * 64 + lane] * fb;
+  l = l * fa + ml.y * fb;
+  m = mn;
+}
+
 // One work item of the streaming kernel, from its first loads to its
 // partial-state stores. `tiles` holds kSplit waves' LDS (Dec::kWaveBytes
 // each); after the step loop the same memory holds each wave's O (16 heads x
 // 128 dims F32 = 8 KiB) for the cross-wave reduction.
 template <typename QE, bool kFp8, int kSplit, int kHT = 1, uint32_t kD = kDim,
-          int kS = kFp8 ? kStreamStagesFp8 : kStreamStages, int kNt = -1>
+          int kS = kFp8 ? kStreamStagesFp8 : kStreamStages, int kNt = -1, bool kPair = false>
 __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item,
-                                            bool preloaded = false, const uint32_t* first_blocks = nullptr) {
+                                            bool preloaded = false, const uint32_t* first_blocks = nullptr,
+                                            uint8_t* partner = nullptr) {
   static_assert(kHT == 1 || kSplit == 1, "two head tiles run one wave per item");
   using Dec = StreamDecoder<QE, kFp8, kHT, kD, kS, kNt>;
   using vec8 = typename Dec::vec8;
@@ -2088,6 +2178,23 @@ __device__ __forceinline__ void stream_item(const DecodeArgs& a, uint8_t* tiles,
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     lt[ht] = l;
+  }
+  if constexpr (kPair) {
+    // Two partitions of one KV head per workgroup (pair_item): the odd one
+    // hands its state to the even one through its own LDS, which combines
+    // them and stores one state for the pair.
+    static_assert(kSplit == 1 && kHT == 1, "pairs run one wave per item");
+    if (partner == nullptr) {
+      pair_publish<Dec>(tiles, dec.m[0], lt[0], dec.acc[0]);
+      __syncthreads();
+      return;
+    }
+    __syncthreads();
+    pair_combine<Dec>(partner, dec.m[0], lt[0], dec.acc[0]);
+    DecodeArgs pairs = a;
+    pairs.parts = (a.parts + 1U) / 2U;  // the states are per pair of partitions
+    if (dec.c < a.group) store_wave_result<QE, kFp8 && Dec::kNtKV>(pairs, dec, 0, seq, kvh * a.group, part / 2U, v_scale, lt[0]);
+    return;
   }
   if (kSplit == 1) {
 #pragma unroll
@@ -2365,7 +2472,8 @@ constexpr int kStreamGroupFp8 = 8;
 // are loaded together: the wave starts after two memory round trips, not
 // three. (Compiler-visible scalar loads: the compiler waits for them before
 // any use or copy.)
-template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim, int kNt = -1, bool kDirect = false>
+template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim, int kNt = -1, bool kDirect = false,
+          bool kPair = false>
 __global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_group_kernel(DecodeArgs a) {
   constexpr int kGroupStages = kFp8 ? kStreamStagesFp8 : kStreamGroupStages;
@@ -2373,7 +2481,28 @@ void decode_stream_group_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t tiles[kGroup * Dec::kWaveBytes];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   LOOM_WAVE_STAMP(blockIdx.x * kGroup + wave);
-  if constexpr (kDirect) {
+  if constexpr (kPair) {
+    // kGroup / 2 adjacent KV heads x two consecutive partitions: waves
+    // w and w + kGroup / 2 hold the same head's partitions 2j and 2j + 1 and
+    // leave one merged state (pair_publish / pair_combine).
+    constexpr uint32_t kHeads = kGroup / 2;
+    const WorkItem item = pair_item(a, blockIdx.x, kHeads, wave);
+    if (item.len == 0) return;  // a unit past the schedule's end: uniform across the workgroup
+    LOOM_WAVE_ITEM(a, item);
+    uint8_t* own = tiles + wave * Dec::kWaveBytes;
+    if (wave >= kHeads) {
+      if (!item.valid) {  // the sequence ends in partition 2j
+        pair_publish_empty<Dec>(own);
+        __syncthreads();
+        return;
+      }
+      stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt, true>(a, own, item);
+    } else {
+      stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt, true>(a, own, item, false, nullptr,
+                                                               tiles + (wave + kHeads) * Dec::kWaveBytes);
+    }
+    return;
+  } else if constexpr (kDirect) {
     uint32_t first[2 * kGroupStages];
     bool preloaded = false;
     const WorkItem item = direct_item<2 * kGroupStages>(a, blockIdx.x * kGroup + wave, first, preloaded);
@@ -2620,6 +2749,7 @@ thread_local std::string g_last_error;
 thread_local const char* g_last_family = "";
 thread_local const char* g_last_kernel = "";  // decode kernel of the last successful call
 thread_local const char* g_launch_kernel = "";  // decode kernel of the launch in progress
+thread_local bool g_launch_pairs = false;       // that launch leaves one state per two partitions
 thread_local uint32_t g_last_internal_split = 0;
 std::atomic<uint64_t> g_decode_launches{0};
 std::atomic<uint64_t> g_rope_launches{0};
@@ -2932,13 +3062,36 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
+// The grouped launch pre-merges pairs of partitions in the workgroup when
+// the call is split (more than two partitions, so the states halve), the
+// workgroup holds eight items (FP8 caches: four adjacent KV heads x two
+// partitions) and the KV heads divide into groups of four. One state per
+// pair of partitions halves the split-K state bytes written, which cost far
+// more than their share of the traffic: on C3 the F32 state stores (10.5 MB,
+// 0.9% of the bytes) cost the decode kernel 17 us of 205 (188 us with the
+// stores sent to 32 KiB of L2-resident lines). Measured: C4 call 201.8 ->
+// 198.4 us; with four-item 16-bit workgroups (two heads x two partitions)
+// C3 went 205.5 -> 206.9 us, the loss of adjacent heads outweighing the
+// halved writes (189 -> 200 us with the stores sent to L2-resident lines).
+bool pair_eligible(const DecodeArgs& a, int group) {
+  return a.parts > 2 && group >= 8 && a.kv_heads % static_cast<uint32_t>(group / 2) == 0;
+}
+
 template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup, int kNt = -1, bool kDirect = false>
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
-  const uint64_t groups = (items + kGroup - 1) / kGroup;
   g_launch_kernel = "decode_stream_group_kernel";
-  hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, kDirect>), dim3(static_cast<uint32_t>(groups)),
-                     dim3(kGroup * 64), 0, stream, args);
+  g_launch_pairs = !kDirect && pair_eligible(args, kGroup);
+  if (g_launch_pairs) {
+    // one workgroup per (sequence, pair of partitions, group of kGroup / 2 KV heads)
+    const uint64_t units = (args.parts + 1ULL) / 2ULL * args.sequences * (args.kv_heads / (kGroup / 2));
+    hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, false, true>),
+                       dim3(static_cast<uint32_t>(units)), dim3(kGroup * 64), 0, stream, args);
+  } else {
+    const uint64_t groups = (items + kGroup - 1) / kGroup;
+    hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, kDirect>),
+                       dim3(static_cast<uint32_t>(groups)), dim3(kGroup * 64), 0, stream, args);
+  }
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
@@ -3162,6 +3315,7 @@ int run_typed(const Problem& p, hipStream_t stream) {
   args.scale_stride = p.scale_stride;
   args.score_scale_log2 = p.scale * kLog2e;
   g_launch_kernel = "";
+  g_launch_pairs = false;
 
   int status = LOOM_HIP_SUCCESS;
   bool use_narrow = false, use_mfma = false, use_heads = false;
@@ -3293,7 +3447,12 @@ int run_typed(const Problem& p, hipStream_t stream) {
                   : use_mfma             ? (stream_eligible(p, parts, group) ? "mfma-stream" : "mfma")
                                          : "vector";
   if (parts > 1) {
-    status = launch_merge<QE>(args, p.sequences * p.query_heads, stream);
+    DecodeArgs merge = args;
+    if (g_launch_pairs) {  // one state per two partitions
+      merge.parts = (args.parts + 1U) / 2U;
+      merge.partition_tokens = 2U * args.partition_tokens;
+    }
+    status = launch_merge<QE>(merge, p.sequences * p.query_heads, stream);
     if (status != LOOM_HIP_SUCCESS) return fail(status, "merge kernel launch failed");
   }
   return LOOM_HIP_SUCCESS;
