@@ -18,8 +18,9 @@
 //                        the group's heads as the N dimension. Full grids
 //                        put four adjacent-head items in one workgroup.
 //   decode_stream_heads_kernel
-//                        groups of 33-128 query heads at D = 64 or 128: one
-//                        wave per 32 heads, all reading one shared LDS ring.
+//                        groups of 17-128 query heads at D = 64 or 128: one
+//                        wave per 16 heads (17-32) or 32 heads (33-128), all
+//                        reading one shared LDS ring.
 //   decode_mfma_kernel   the same head layout with 32-token chunks and K in
 //                        registers, for block sizes below 16 and partitions
 //                        that are not a multiple of 16 tokens.
@@ -2265,15 +2266,15 @@ constexpr int kSharedStages = 4;
 // stage and shows that every wave has finished the previous step, whose
 // stage wave 0 then refills (S - 1 steps ahead). The waves have the same
 // steps, so all of them reach every barrier.
-template <typename QE, bool kFp8, int kWaves, uint32_t kD>
+template <typename QE, bool kFp8, int kWaves, uint32_t kD, int kHTW = 2>
 __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t* tiles, const WorkItem& item) {
-  using Dec = StreamDecoder<QE, kFp8, 2, kD>;
+  using Dec = StreamDecoder<QE, kFp8, kHTW, kD>;
   using vec8 = typename Dec::vec8;
   constexpr int S = kSharedStages;
   const uint32_t kvh = item.kvh, part = item.part, seq = item.seq, len = item.len;
   const uint32_t p0 = part * a.partition_tokens;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t h0 = wave * 32U;
+  const uint32_t h0 = wave * 16U * kHTW;
 
   Dec dec(a);
   dec.lane = threadIdx.x & 63U;
@@ -2300,7 +2301,7 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
   }
   dec.sl2 = a.score_scale_log2 * k_scale;
 #pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
+  for (int ht = 0; ht < kHTW; ++ht) {
     dec.m[ht] = -INFINITY;
     dec.lsum[ht] = 0.0f;
 #pragma unroll
@@ -2328,9 +2329,9 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
     }
   }
   {
-    u32x4 qw[2][Dec::kKc];
+    u32x4 qw[kHTW][Dec::kKc];
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
+    for (int ht = 0; ht < kHTW; ++ht) {
       const uint32_t h = min(h0 + ht * 16U + dec.c, a.group - 1U);  // rows >= group are zeroed below
       const uint16_t* qrow = static_cast<const uint16_t*>(a.query) +
                              (static_cast<uint64_t>(seq) * a.query_heads + kvh * a.group + h) * kD;
@@ -2342,12 +2343,12 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
     }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
+    for (int ht = 0; ht < kHTW; ++ht) {
 #pragma unroll
       for (int kc = 0; kc < Dec::kKc; ++kc) asm volatile("" : "+v"(qw[ht][kc]));  // loaded: the wait above was vmcnt(0)
     }
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
+    for (int ht = 0; ht < kHTW; ++ht) {
       const bool live = h0 + ht * 16U + dec.c < a.group;
 #pragma unroll
       for (int kc = 0; kc < Dec::kKc; ++kc)
@@ -2378,7 +2379,7 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
           dec.stage_v_fp8(stage, vtile, t0);
           wave_fence_lds();
         }
-        f32x4 sc[2];
+        f32x4 sc[kHTW];
         dec.qk(stage, sc);
         dec.softmax_pv(sc, t0, vtile);
       }
@@ -2387,7 +2388,7 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
   if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 
 #pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
+  for (int ht = 0; ht < kHTW; ++ht) {
     float l = dec.lsum[ht];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -2521,15 +2522,15 @@ void decode_stream_group_kernel(DecodeArgs a) {
 // Groups of 33-128 query heads: one workgroup of ceil(group / 32) waves per
 // work item (stream_item_shared), so that each K/V row is read from HBM once
 // into LDS for all of the group's heads.
-template <typename QE, bool kFp8, int kWaves, uint32_t kD = kDim>
+template <typename QE, bool kFp8, int kWaves, uint32_t kD = kDim, int kHTW = 2>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_heads_kernel(DecodeArgs a) {
-  using Dec = StreamDecoder<QE, kFp8, 2, kD>;
+  using Dec = StreamDecoder<QE, kFp8, kHTW, kD>;
   __shared__ __attribute__((aligned(16)))
   uint8_t tiles[kSharedStages * Dec::kStageBytes + (kFp8 ? kWaves * kStep * Dec::kPitch : 0)];
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
-  stream_item_shared<QE, kFp8, kWaves, kD>(a, tiles, item);
+  stream_item_shared<QE, kFp8, kWaves, kD, kHTW>(a, tiles, item);
 }
 
 // ---------------------------------------------------------------------------
@@ -3202,6 +3203,20 @@ int launch_stream_heads(const DecodeArgs& args, uint64_t items, uint32_t group, 
   return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
 }
 
+// Groups of 17-32 query heads as two waves of 16 heads on one shared ring of
+// K/V stages (decode_stream_heads_kernel with one head tile per wave). With
+// PV taking BF16 probabilities as hi + lo, a wave holding both head tiles
+// became bound by its own MFMA and softmax chain at ~3 waves per CU: C5
+// decode 74.7 us as one wave per item, 70.2 us as two.
+template <typename QE, bool kFp8, uint32_t kD>
+int launch_stream_heads2(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
+  TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
+  g_launch_kernel = "decode_stream_heads_kernel";
+  hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 2, kD, 1>), dim3(static_cast<uint32_t>(items)), dim3(128), 0,
+                     stream, args);
+  return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+}
+
 bool narrow_stream_eligible(const Problem& p, uint64_t parts, uint32_t group) {
   if (!narrow_shape(p.dtype, p.cache_encoding, p.head_size, p.value_head_size, p.query_heads, p.kv_heads,
                     p.block_size) &&
@@ -3374,8 +3389,8 @@ int run_typed(const Problem& p, hipStream_t stream) {
                        : launch_stream<QE, false, 4, 1, 256>(args, grid, stream);
         }
       } else if (group > 16) {
-        status = fp8 ? launch_stream<QE, true, 1, 2, 64>(args, grid, stream)
-                     : launch_stream<QE, false, 1, 2, 64>(args, grid, stream);
+        status = fp8 ? launch_stream_heads2<QE, true, 64>(args, grid, stream)
+                     : launch_stream_heads2<QE, false, 64>(args, grid, stream);
       } else if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
         status = fp8 ? (dense_rows ? launch_stream_group<QE, true, 64, kStreamGroupFp8, 1>(args, grid, stream)
                                    : launch_stream_group<QE, true, 64, kStreamGroupFp8>(args, grid, stream))
@@ -3408,7 +3423,8 @@ int run_typed(const Problem& p, hipStream_t stream) {
       // co-locating heads. (16-wave groups measured slower: they add no CUs,
       // only contention within one.)
       if (group > 16) {
-        status = fp8 ? launch_stream<QE, true, 1, 2>(args, grid, stream) : launch_stream<QE, false, 1, 2>(args, grid, stream);
+        status = fp8 ? launch_stream_heads2<QE, true, kDim>(args, grid, stream)
+                     : launch_stream_heads2<QE, false, kDim>(args, grid, stream);
       } else if (grid >= 4096 || (grid >= 1024 && steps >= 8)) {
         // The library's own split runs its items in index order with each
         // item's first block IDs loaded alongside its length (C2 decode
