@@ -117,6 +117,8 @@ SIGNATURES = {
     "loom_hip_last_kernel_family": ([], ctypes.c_char_p),
     "loom_hip_last_internal_partition_tokens": ([], ctypes.c_uint32),
     "loom_hip_last_kernel_name": ([], ctypes.c_char_p),
+    "loom_hip_paged_decode_attention_plan": ([U32] * 8 + [ctypes.c_void_p, ctypes.POINTER(U32), ctypes.POINTER(U32)],
+                                             ctypes.c_int),
     "loom_hip_launch_count": ([U32, ctypes.POINTER(U64)], ctypes.c_int),
     "loom_hip_reset_launch_count": ([U32], ctypes.c_int),
     "loom_hip_kernel_timing_enable": ([U32], ctypes.c_int),

@@ -3586,8 +3586,9 @@ bool internal_split_enabled() {
 }
 
 // The slot of `stream` on the current device, claiming a free one on the
-// stream's first call; nullptr when the call runs as one partition.
-float* stream_slot(hipStream_t stream) {
+// stream's first call (claim = false: only whether it has or would get one,
+// non-null then); nullptr when the call runs as one partition.
+float* stream_slot(hipStream_t stream, bool claim = true) {
   if (stream == hipStreamPerThread) return nullptr;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
@@ -3624,6 +3625,7 @@ float* stream_slot(hipStream_t stream) {
     if (pool.owner[i] == stream) pick = i;
   if (pick < 0) {
     if (pool.owners == kPoolSlots) return nullptr;
+    if (!claim) return pool.base;
     pick = pool.owners++;
     pool.owner[pick] = stream;
   }
@@ -3858,6 +3860,34 @@ const char* loom_hip_last_kernel_family(void) { return g_last_family; }
 uint32_t loom_hip_last_internal_partition_tokens(void) { return g_last_internal_split; }
 
 const char* loom_hip_last_kernel_name(void) { return g_last_kernel; }
+
+int loom_hip_paged_decode_attention_plan(uint32_t dtype, uint32_t sequences, uint32_t query_heads, uint32_t kv_heads,
+                                         uint32_t head_size, uint32_t value_head_size, uint32_t max_sequence_length,
+                                         uint32_t partition_tokens, void* stream, uint32_t* run_partition_tokens,
+                                         uint32_t* internal_split) {
+  if (run_partition_tokens == nullptr || internal_split == nullptr)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "plan outputs must be non-null");
+  if (dtype > kBf16 || sequences == 0 || query_heads == 0 || kv_heads == 0 || head_size == 0 ||
+      value_head_size == 0 || max_sequence_length == 0 || query_heads % kv_heads != 0)
+    return fail(LOOM_HIP_INVALID_ARGUMENT, "plan shape is invalid");
+  *internal_split = 0;
+  *run_partition_tokens = parts_for(max_sequence_length, partition_tokens) > 1 ? partition_tokens : 0;
+  if (*run_partition_tokens != 0) return LOOM_HIP_SUCCESS;
+  Problem p{};
+  p.sequences = sequences;
+  p.query_heads = query_heads;
+  p.kv_heads = kv_heads;
+  p.head_size = head_size;
+  p.value_head_size = value_head_size;
+  p.max_sequence_length = max_sequence_length;
+  const uint32_t t = internal_partition_tokens(p);
+  if (t != 0 && internal_split_enabled() && device_available() == LOOM_HIP_SUCCESS &&
+      stream_slot(static_cast<hipStream_t>(stream), false) != nullptr) {
+    *run_partition_tokens = t;
+    *internal_split = 1;
+  }
+  return LOOM_HIP_SUCCESS;
+}
 
 int loom_hip_launch_count(uint32_t operation, uint64_t* count) {
   if ((operation != LOOM_HIP_PAGED_DECODE_ATTENTION && operation != LOOM_HIP_ROPE_PAGED_KV_WRITE) ||

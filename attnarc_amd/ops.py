@@ -491,6 +491,27 @@ def last_kernel_name() -> str:
     return _native.lib().loom_hip_last_kernel_name().decode()
 
 
+def plan(dtype: int, sequences: int, query_heads: int, kv_heads: int, head_size: int, value_head_size: int,
+         max_sequence_length: int, partition_tokens: int = 0, stream=None) -> tuple[int, bool]:
+    """(partition tokens the call would run with, whether that is the
+    library's internal split) for a paged-decode call on ``stream`` (a torch
+    stream or raw handle; the current stream by default), without a launch."""
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    elif hasattr(stream, "cuda_stream"):
+        stream = stream.cuda_stream
+    run = ctypes.c_uint32()
+    internal = ctypes.c_uint32()
+    _native.check(
+        _native.lib().loom_hip_paged_decode_attention_plan(
+            dtype, sequences, query_heads, kv_heads, head_size, value_head_size, _abi_u32(max_sequence_length),
+            _abi_u32(partition_tokens, "partition size"), ctypes.c_void_p(stream), ctypes.byref(run),
+            ctypes.byref(internal)),
+        "paged decode plan",
+    )
+    return int(run.value), bool(internal.value)
+
+
 def launch_count(operation: int = _native.PAGED_DECODE_ATTENTION) -> int:
     count = ctypes.c_uint64()
     _native.check(_native.lib().loom_hip_launch_count(operation, ctypes.byref(count)), "launch count")

@@ -84,44 +84,6 @@ def _probe_once(lib, kind, src, dst, sink, nbytes, blocks, stream, iters):
     return moved / sec / 1e9
 
 
-PROBE_POLICIES = {0: "plain 16-byte loads", 1: "non-temporal 16-byte loads", 2: "LDS DMA",
-                  3: "LDS DMA, non-temporal"}
-
-
-def policy_probe(policy: int, nbytes: int = 4 << 30, iters: int = 10, per_cu=(2, 4, 8)) -> dict:
-    """Read rate of 4 GiB in contiguous per-workgroup ranges under one load
-    policy (``PROBE_POLICIES``), per grid size; the evidence for the decode
-    kernels' non-temporal K/V loads."""
-    import ctypes
-
-    import torch
-
-    from attnarc_amd import build as _b
-
-    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
-    fn = lib.loom_hip_probe_policy_read
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
-                   ctypes.c_void_p]
-    props = torch.cuda.get_device_properties(0)
-    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
-    sink = torch.empty(props.multi_processor_count * max(per_cu) * 256, dtype=torch.int32, device="cuda")
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    rates = {}
-    for k in per_cu:
-        blocks = props.multi_processor_count * k
-        assert fn(src.data_ptr(), nbytes, sink.data_ptr(), blocks, policy, stream) == 0
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(iters):
-            fn(src.data_ptr(), nbytes, sink.data_ptr(), blocks, policy, stream)
-        b.record()
-        torch.cuda.synchronize()
-        rates[k] = round(nbytes * iters / (a.elapsed_time(b) * 1e-3) / 1e9, 1)
-    return rates
-
-
 def gather_read_probe(chunk_bytes: int = 16384, nbytes: int = 2 << 30, iters: int = 5,
                       per_cu=(2, 4, 8)) -> float:
     """Attainable rate of a paged access pattern: ``nbytes`` read as randomly
@@ -163,36 +125,6 @@ def gather_read_probe(chunk_bytes: int = 16384, nbytes: int = 2 << 30, iters: in
         torch.cuda.synchronize()
         best = max(best, nbytes * iters / (a.elapsed_time(b) * 1e-3) / 1e9)
     return best
-
-
-def slice_probe(workgroups: int, nbytes: int = 64 << 20, copies: int = 16, iters: int = 20) -> float:
-    """Read rate of ``workgroups`` 512-thread workgroups (one per CU), each
-    streaming a contiguous slice; ``copies`` rotated buffers keep the reads out
-    of the Infinity Cache."""
-    import ctypes
-
-    import torch
-
-    from attnarc_amd import build as _b
-
-    lib = ctypes.CDLL(_b.PROBE_LIB_PATH)
-    lib.loom_hip_probe_slice_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint32,
-                                              ctypes.c_void_p]
-    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(copies)]
-    sink = torch.empty(workgroups * 512, dtype=torch.int32, device="cuda")
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    nb = nbytes - nbytes % (16 * workgroups)
-    for i in range(copies):
-        assert lib.loom_hip_probe_slice_read(bufs[i].data_ptr(), nb, sink.data_ptr(), workgroups, stream) == 0
-    torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(iters):
-        assert lib.loom_hip_probe_slice_read(bufs[i % copies].data_ptr(), nb, sink.data_ptr(), workgroups, stream) == 0
-    b.record()
-    torch.cuda.synchronize()
-    return nb * iters / (a.elapsed_time(b) * 1e-3) / 1e9
 
 
 def cpu_model() -> str:
@@ -537,7 +469,7 @@ def main() -> int:
     ap.add_argument("--shape", default=None,
                     help="a decode workload other than the five configurations, e.g. "
                          "'B=64,Hq=16,Hkv=8,D=256,L=2048,part=512' (see workloads.shape_case); not the metric")
-    ap.add_argument("--probe", choices=["read", "copy", "slice", "policies"], default=None,
+    ap.add_argument("--probe", choices=["read", "copy"], default=None,
                     help="only run the HBM probe kernel (for counter calibration) and print GB/s")
     args = ap.parse_args()
 
@@ -557,16 +489,6 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.probe == "policies":
-        for policy, name in PROBE_POLICIES.items():
-            print(json.dumps({"probe": "policies", "policy": name, "bytes": 4 << 30,
-                              "GB/s by workgroups per CU": policy_probe(policy)}), flush=True)
-        return 0
-    if args.probe == "slice":
-        for wgs in (64, 128, 256, 512):
-            print(json.dumps({"probe": "slice", "workgroups": wgs, "threads": 512, "bytes": 64 << 20,
-                              "GB/s": round(slice_probe(wgs), 1)}), flush=True)
-        return 0
     if args.probe:
         print(json.dumps({"probe": args.probe, "bytes": 4 << 30, "GB/s": round(hbm_probe(args.probe), 1)}))
         return 0
@@ -645,6 +567,7 @@ def main() -> int:
     # A single-partition call on a small grid is split inside the library
     # (eager calls only; a captured call keeps one partition).
     internal_pt = ops.last_internal_partition_tokens()
+    kernel_name = ops.last_kernel_name()  # the decode kernel these calls launched
     dec_us = dec_ms / max(dec_n, 1) * 1e3
     mrg_us = mrg_ms / max(mrg_n, 1) * 1e3 if mrg_n else 0.0
     achieved = kv_bytes / (dec_us * 1e-6) / 1e9
@@ -689,28 +612,6 @@ def main() -> int:
     peak_read = hbm_probe("read")
     block_bytes = case.block_size * case.kv_heads * case.head_size * case.kv_elem_bytes
     gather_read = gather_read_probe(block_bytes)
-
-    enc = _native.KV_CACHE_FP8_E4M3 if case.cache_encoding == "fp8" else _native.KV_CACHE_NATIVE
-    qdt = {torch.float32: _native.F32, torch.float16: _native.F16, torch.bfloat16: _native.BF16}[case.dtype]
-    _, _, family = ops.supports(qdt, enc, case.sequences, case.query_heads, case.kv_heads, case.head_size,
-                                case.value_head_size, case.num_blocks, case.block_size,
-                                case.max_blocks_per_sequence, case.max_sequence_length, case.scale)
-    if family == "mfma-stream" and case.partition_tokens % 16 != 0:
-        family = "mfma"
-    kernel_name = {"mfma-stream": "decode_stream_kernel", "mfma": "decode_mfma_kernel"}.get(family,
-                                                                                          "decode_vector_kernel")
-    if family == "mfma-stream":
-        # the library's launch rule: grouped single-wave items for >= 4096 work items, or >= 1024
-        # with partitions of 8+ steps of 16 tokens (head size 256: >= 4096 only); none for groups
-        # of more than 16 query heads
-        pt = internal_pt or case.partition_tokens or case.max_sequence_length
-        items = -(-case.max_sequence_length // pt) * case.kv_heads * case.sequences
-        steps = -(-pt // 16)
-        grouped = items >= 4096 or (items >= 1024 and steps >= 8 and case.head_size != 256)
-        if case.query_heads // case.kv_heads > 32:
-            kernel_name = "decode_stream_heads_kernel"  # one wave per 32 heads of the group
-        elif grouped and case.query_heads // case.kv_heads <= 16:
-            kernel_name = "decode_stream_group_kernel"
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -387,6 +387,31 @@ const char* loom_hip_last_kernel_family(void);
 uint32_t loom_hip_last_internal_partition_tokens(void);
 
 /*
+ * Plan of a paged decode call on `stream`, without launching anything:
+ * *run_partition_tokens is the partition size the call would run with
+ * (partition_tokens itself for a split call; for a single-partition call,
+ * the internal split's size when the call would take it, else 0), and
+ * *internal_split is 1 when that size comes from the internal split. A
+ * single-partition call takes the internal split when its (sequence, KV
+ * head) items cannot fill the GPU, its context reaches 2048 tokens, the
+ * environment variable LOOM_HIP_INTERNAL_SPLIT is not "0", and `stream` owns
+ * one of the library's 4 slots or a free slot remains (the query does not
+ * claim one; hipStreamPerThread and capturing streams never take a slot).
+ * Library-held state behind this: split_pool, a static device array of
+ * 4 slots x 16 MiB per device, and the no-allocation entry point's 64 MiB
+ * array, both resident from module load until the process ends (128 MiB of
+ * HBM per device). No reference counterpart: the reference keeps no state
+ * beyond counters and the last error (cuda/mod.rs:45-52).
+ */
+int loom_hip_paged_decode_attention_plan(uint32_t dtype, uint32_t sequences,
+                                         uint32_t query_heads, uint32_t kv_heads,
+                                         uint32_t head_size, uint32_t value_head_size,
+                                         uint32_t max_sequence_length,
+                                         uint32_t partition_tokens, void* stream,
+                                         uint32_t* run_partition_tokens,
+                                         uint32_t* internal_split);
+
+/*
  * Name of the decode kernel that the last successful paged decode call on
  * this thread launched ("decode_stream_group_kernel", "decode_stream_kernel",
  * "decode_stream_heads_kernel", "decode_mfma_kernel" or

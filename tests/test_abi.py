@@ -310,3 +310,20 @@ def test_no_alloc_rejects_unknown_dtype():
 @no_device
 def test_no_alloc_valid_call_needs_a_device():
     assert call_no_alloc(maxlen=256, part=64) == _native.UNAVAILABLE
+
+
+def test_plan_query_on_the_host():
+    """The plan of a split call needs no device; invalid shapes and null
+    outputs are rejected; with no device a single-partition call plans one
+    partition (the internal split needs a device and a stream slot)."""
+    lib = _native.lib()
+    run, internal = ctypes.c_uint32(7), ctypes.c_uint32(7)
+    args = [_native.BF16, 4, 32, 8, 128, 128, 4096]
+    assert lib.loom_hip_paged_decode_attention_plan(*args, 512, None, ctypes.byref(run), ctypes.byref(internal)) == 0
+    assert (run.value, internal.value) == (512, 0)
+    assert lib.loom_hip_paged_decode_attention_plan(*args, 0, None, None, ctypes.byref(internal)) == 1
+    bad = [_native.BF16, 4, 30, 8, 128, 128, 4096]  # 30 query heads over 8 KV heads
+    assert lib.loom_hip_paged_decode_attention_plan(*bad, 0, None, ctypes.byref(run), ctypes.byref(internal)) == 1
+    if not torch.cuda.is_available():
+        assert lib.loom_hip_paged_decode_attention_plan(*args, 0, None, ctypes.byref(run), ctypes.byref(internal)) == 0
+        assert (run.value, internal.value) == (0, 0)

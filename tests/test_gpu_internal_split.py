@@ -214,3 +214,31 @@ def test_internal_split_on_the_general_kernel():
     expected, want_lse = oracle_expected(case)
     assert_parity(out, expected, torch.float16, "internal split, general kernel")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
+
+
+def test_plan_query_agrees_with_the_calls():
+    """loom_hip_paged_decode_attention_plan answers, without a launch, what the
+    call then does: the internal split's size on this stream, the caller's
+    partitions for a split call, one partition for a large grid or under
+    capture."""
+    bf16 = _native.BF16
+    case = _case(18)
+    run, internal = ops.plan(bf16, case.sequences, case.query_heads, case.kv_heads, 128, 128,
+                             case.max_sequence_length)
+    workloads.run_case(case)
+    torch.cuda.synchronize()
+    assert (run, internal) == (ops.last_internal_partition_tokens(), run != 0)
+    assert ops.plan(bf16, 4, 12, 2, 128, 128, 2048, partition_tokens=512) == (512, False)
+    assert ops.plan(bf16, 32, 64, 8, 128, 128, 1024) == (0, False)  # 256 items fill the GPU
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    out = torch.empty(case.sequences, case.query_heads, 128, dtype=torch.bfloat16, device=DEV)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        workloads.run_case(case, output=out)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        assert ops.plan(bf16, case.sequences, case.query_heads, case.kv_heads, 128, 128,
+                        case.max_sequence_length) == (0, False)
+        workloads.run_case(case, output=out)
+    assert ops.last_internal_partition_tokens() == 0
