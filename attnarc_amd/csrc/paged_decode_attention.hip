@@ -2519,9 +2519,9 @@ void decode_stream_group_kernel(DecodeArgs a) {
 }
 
 
-// Groups of 33-128 query heads: one workgroup of ceil(group / 32) waves per
-// work item (stream_item_shared), so that each K/V row is read from HBM once
-// into LDS for all of the group's heads.
+// Groups of 17-128 query heads: one workgroup of waves of 16 or 32 heads each
+// (kHTW head tiles of 16) per work item (stream_item_shared), so that each K/V
+// row is read from HBM once into LDS for all of the group's heads.
 template <typename QE, bool kFp8, int kWaves, uint32_t kD = kDim, int kHTW = 2>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_stream_heads_kernel(DecodeArgs a) {
@@ -3162,7 +3162,7 @@ bool rot_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint
 }
 
 // Groups of 33-128 query heads at head size 64 or 128, native or FP8 cache:
-// the streaming kernel with one wave per 32 heads of the group.
+// the streaming kernel with one wave per 16 or 32 heads of the group.
 bool heads_shape(uint32_t dtype, uint32_t cache_encoding, uint32_t head_size, uint32_t value_head_size,
                  uint32_t query_heads, uint32_t kv_heads, uint32_t block_size) {
   const uint32_t group = query_heads / kv_heads;
@@ -3193,6 +3193,27 @@ int launch_stream_heads(const DecodeArgs& args, uint64_t items, uint32_t group, 
   static_assert(4 * Dec::kWaveBytes <= 64 * 1024, "four waves' stages fit in 64 KiB of LDS");
   const dim3 grid(static_cast<uint32_t>(items));
   g_launch_kernel = "decode_stream_heads_kernel";
+  // One head tile per wave for 16-bit caches up to 64 heads (BF16 PV splits
+  // probabilities into hi + lo, two MFMAs per tile; F16 48/1 and 64/1 gain
+  // 3.5 us as well), and for FP8 groups of up to 48 heads, whose second wave
+  // would otherwise hold a half-empty tile. Decode us, two-tile waves ->
+  // one-tile waves (B=64, 16384 tokens, 512-token partitions): BF16 48/1
+  // 120.4 -> 109.7, 64/1 124.5 -> 112.9, head size 64 48/1 62.2 -> 56.0;
+  // FP8 48/1 102.8 -> 98.3, FP8 64/1 105.6 -> 107.1 (kept on two tiles).
+  if ((!kFp8 && group <= 64) || group <= 48) {
+    if (group <= 48)
+      hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 3, kD, 1>), grid, dim3(192), 0, stream, args);
+    else
+      hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 4, kD, 1>), grid, dim3(256), 0, stream, args);
+    return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+  }
+  // 16-bit caches with groups of 97-128: eight one-tile waves (BF16 128/1,
+  // 8192 tokens: 93.3 -> 88.4 us). Groups of 65-96 stay on three two-tile
+  // waves: six one-tile waves took 102 us against 70.
+  if (!kFp8 && group > 96) {
+    hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 8, kD, 1>), grid, dim3(512), 0, stream, args);
+    return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+  }
   if (group <= 64) {
     hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 2, kD>), grid, dim3(128), 0, stream, args);
   } else if (group <= 96) {

@@ -320,15 +320,17 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
 @pytest.mark.parametrize("encoding", ["native", "fp8"])
 @pytest.mark.parametrize("layout", ["NHD", "HND"])
 @pytest.mark.parametrize("shape,partition_tokens", [
-    ((3, 64, 1, 128, 128, 16, [1100, 1, 530]), 512),       # MQA group of 64: two waves
-    ((2, 96, 2, 128, 128, 16, [700, 2049]), 256),          # group of 48: second wave half live
-    ((2, 128, 1, 128, 128, 32, [33, 900]), 0),             # group of 128: four waves, one partition
+    ((3, 64, 1, 128, 128, 16, [1100, 1, 530]), 512),       # MQA group of 64: four 16-head waves (FP8: two 32-head)
+    ((2, 96, 2, 128, 128, 16, [700, 2049]), 256),          # group of 48: three 16-head waves
+    ((2, 128, 1, 128, 128, 32, [33, 900]), 0),             # group of 128: eight 16-head waves (FP8: four 32-head), one partition
     ((3, 71, 1, 64, 64, 16, [513, 17, 1600]), 512),        # group of 71 at head size 64: three waves, the last 7 heads live
-    ((2, 80, 2, 64, 64, 16, [640, 90]), 64),               # group of 40, 64-token partitions
+    ((2, 80, 2, 64, 64, 16, [640, 90]), 64),               # group of 40, 64-token partitions: the third wave 8 heads live
+    ((2, 33, 1, 128, 128, 16, [300, 1500]), 256),          # group of 33: the third wave one head live
+    ((2, 100, 1, 64, 64, 16, [1000, 70]), 128),            # group of 100: the eighth 16-head wave 4 heads live
 ])
 def test_stream_kernel_wide_groups(dtype, encoding, layout, shape, partition_tokens):
     """Groups of 33-128 query heads per KV head: one workgroup per item, each
-    wave computing 32 heads of the group from the same K/V rows."""
+    wave computing 16 or 32 heads of the group from the same K/V rows."""
     B, Hq, Hkv, D, Dv, bs, lengths = shape
     case = case_from(shape, dtype, seed=81, layout=layout, partition_tokens=partition_tokens,
                      cache_encoding=encoding)
