@@ -1775,8 +1775,9 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
   // dispatcher deals workgroups to the XCDs in turn, and with the head
   // varying fastest each XCD would otherwise read the same half of every
   // token row (the XCDs holding the second half finished up to 15 us later;
-  // C3 call 205.2 -> 204.8 us).
-  if ((a.kv_heads & 1U) == 0 && (pair & 1U)) it.kvh ^= a.kv_heads / 2;
+  // C3 call 205.2 -> 204.8 us). XOR with kv_heads / 2 is a permutation of
+  // the heads only when kv_heads is a power of two (6 heads would map 4 to 7).
+  if (a.kv_heads >= 2 && (a.kv_heads & (a.kv_heads - 1U)) == 0 && (pair & 1U)) it.kvh ^= a.kv_heads / 2;
   // Class 0: full partitions (len / pt per sequence); class 1: one partial
   // last partition per sequence whose length is not a multiple of pt.
   uint32_t before = 0;  // pairs of earlier classes and chunks

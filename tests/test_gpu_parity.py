@@ -488,3 +488,24 @@ def test_config_full_against_oracle_and_split_invariance(index):
         assert bool((diff <= bound).all()), f"partition {other}: max diff {diff.max().item()}"
         assert torch.allclose(lse2, lse, atol=1e-4, rtol=1e-5)
     assert math.isfinite(float(out.float().abs().max()))
+
+
+@pytest.mark.parametrize("encoding", ["native", "fp8"])
+@pytest.mark.parametrize("shape,partition_tokens,kernel", [
+    ((48, 24, 6, 128, 128, 16, [700 + 9 * i for i in range(48)]), 128, "decode_stream_group_kernel"),
+    ((3, 12, 6, 128, 128, 16, [300, 1000, 50]), 256, "decode_stream_kernel"),
+    ((5, 24, 12, 64, 64, 16, [513, 1, 1024, 77, 900]), 128, "decode_stream_kernel"),
+    ((2, 288, 6, 128, 128, 16, [600, 1300]), 256, "decode_stream_heads_kernel"),
+])
+def test_kv_head_counts_that_are_not_powers_of_two(encoding, shape, partition_tokens, kernel):
+    """6 and 12 KV heads on the scheduled streaming kernels. Odd (sequence,
+    partition) pairs swap the halves of the KV heads only when their count is
+    a power of two: XOR with half of 6 would send head 4 to 7 and never
+    compute heads 4 and 5."""
+    case = case_from(shape, torch.bfloat16, seed=91, partition_tokens=partition_tokens, cache_encoding=encoding)
+    out, lse = workloads.run_case(case, return_lse=True)
+    torch.cuda.synchronize()
+    assert ops.last_kernel_name() == kernel
+    expected, want_lse = oracle_expected(case)
+    assert_parity(out, expected, torch.bfloat16, f"{shape[:3]} {encoding}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
