@@ -2474,6 +2474,20 @@ constexpr int kStreamGroupFp8 = 8;
 // are loaded together: the wave starts after two memory round trips, not
 // three. (Compiler-visible scalar loads: the compiler waits for them before
 // any use or copy.)
+// Wave priority rising with the workgroup's place in the grid, in four steps
+// (s_setprio 0-3): of the waves on one CU, those dispatched later, which run
+// the schedule's last and shortest items, get the issue slots first, so the
+// launch's tail is shorter. C3 call 205.3 -> 204.2 us (three pairs, one box);
+// wide groups (B=64, 16384 tokens) BF16 48/1 126.5 -> 124.1, FP8 64/1
+// 127.0 -> 125.1. The FP8 two-partition workgroups measured 0.9 us slower
+// with it (C4) and keep the default priority.
+__device__ __forceinline__ void rise_priority_with_dispatch() {
+  const uint32_t q = blockIdx.x * 4U / gridDim.x;
+  if (q == 1) __builtin_amdgcn_s_setprio(1);
+  else if (q == 2) __builtin_amdgcn_s_setprio(2);
+  else if (q == 3) __builtin_amdgcn_s_setprio(3);
+}
+
 template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim, int kNt = -1, bool kDirect = false,
           bool kPair = false>
 __global__ __launch_bounds__(kGroup * 64) __attribute__((amdgpu_waves_per_eu(2)))
@@ -2512,6 +2526,7 @@ void decode_stream_group_kernel(DecodeArgs a) {
     LOOM_WAVE_ITEM(a, item);
     stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item, preloaded, first);
   } else {
+    rise_priority_with_dispatch();
     const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
     LOOM_WAVE_ITEM(a, item);
     if (!item.valid) return;  // per wave: nothing below waits on the other waves
@@ -2529,6 +2544,7 @@ void decode_stream_heads_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8, kHTW, kD>;
   __shared__ __attribute__((aligned(16)))
   uint8_t tiles[kSharedStages * Dec::kStageBytes + (kFp8 ? kWaves * kStep * Dec::kPitch : 0)];
+  rise_priority_with_dispatch();
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (!item.valid) return;  // uniform across the workgroup
   stream_item_shared<QE, kFp8, kWaves, kD, kHTW>(a, tiles, item);
@@ -3075,8 +3091,12 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
 // 198.4 us; with four-item 16-bit workgroups (two heads x two partitions)
 // C3 went 205.5 -> 206.9 us, the loss of adjacent heads outweighing the
 // halved writes (189 -> 200 us with the stores sent to L2-resident lines).
+// Head size 128 only. Call us, pairs against one state per partition
+// (B=64, Hq 32 / Hkv 8, 512-token partitions, NHD): FP8 head size 64 117.1
+// against 115.3, 80 134.2 against 132.7, 96 131.2 against 129.3, 112 105.5
+// against 104.4, 128 102.9 against 102.9; C4 (HND, 128) 3.4 faster.
 bool pair_eligible(const DecodeArgs& a, int group) {
-  return a.parts > 2 && group >= 8 && a.kv_heads % static_cast<uint32_t>(group / 2) == 0;
+  return a.head_size == kDim && a.parts > 2 && group >= 8 && a.kv_heads % static_cast<uint32_t>(group / 2) == 0;
 }
 
 template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup, int kNt = -1, bool kDirect = false>

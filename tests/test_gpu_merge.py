@@ -125,10 +125,11 @@ def test_length_past_max_sequence_length_stays_in_its_share(hq, hkv, dtype):
 
 @pytest.mark.parametrize("head,layout", [(128, "HND"), (128, "NHD"), (64, "HND")])
 def test_fp8_two_partition_workgroups(head, layout):
-    """FP8 grids of 1024+ items run eight-item workgroups of four KV heads x
-    two partitions that leave one state per pair: sequences that end inside
-    the first partition of a pair, exactly on a pair boundary, one token past
-    it, and single-token ones."""
+    """FP8 grids of 1024+ items at head size 128 run eight-item workgroups of
+    four KV heads x two partitions that leave one state per pair (head size
+    64: one state per partition): sequences that end inside the first
+    partition of a pair, exactly on a pair boundary, one token past it, and
+    single-token ones."""
     rng = np.random.default_rng(head)
     lengths = [int(x) for x in rng.integers(1, 4097, 40)]
     lengths[:8] = [1, 511, 512, 513, 1024, 1025, 2048, 4096]
