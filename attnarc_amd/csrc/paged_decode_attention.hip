@@ -2357,7 +2357,9 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
     }
   }
 
+  LOOM_WAVE_STALL_DECL;
   for (uint32_t n = 0; n < nst; n += S) {
+    if (wave == 0) LOOM_WAVE_MARK(n, S, nst);
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       if (n + i < nst) {
@@ -2366,7 +2368,7 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
         const int j = (i + S - 1) % S;  // the stage of the previous step
         if (wave == 0) {
           // this step's loads; the later steps' (up to S - 2) stay in flight
-          vm_wait_dma_later<Dec::kDmaPerStep, S - 2>(nst - 1 - (n + i));
+          LOOM_WAVE_STALL(n + i, nst, (vm_wait_dma_later<Dec::kDmaPerStep, S - 2>(nst - 1 - (n + i))));
           if (!kFp8) dec.zero_dead_rows(stage + Dec::kVOff, t0);
         }
         lds_barrier();  // this step's stage is in LDS; every wave is done with the previous one
@@ -2386,7 +2388,10 @@ __device__ __forceinline__ void stream_item_shared(const DecodeArgs& a, uint8_t*
       }
     }
   }
-  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  if (wave == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    LOOM_WAVE_STALL_STORE;
+  }
 
 #pragma unroll
   for (int ht = 0; ht < kHTW; ++ht) {
@@ -2545,7 +2550,9 @@ void decode_stream_heads_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16)))
   uint8_t tiles[kSharedStages * Dec::kStageBytes + (kFp8 ? kWaves * kStep * Dec::kPitch : 0)];
   rise_priority_with_dispatch();
+  LOOM_WAVE_STAMP(blockIdx.x * kWaves + (threadIdx.x >> 6));
   const WorkItem item = schedule_item(a, blockIdx.x);
+  if (threadIdx.x < 64) LOOM_WAVE_ITEM(a, item);  // one record per item: the waves share its K/V reads
   if (!item.valid) return;  // uniform across the workgroup
   stream_item_shared<QE, kFp8, kWaves, kD, kHTW>(a, tiles, item);
 }
