@@ -3235,11 +3235,15 @@ int launch_stream_heads(const DecodeArgs& args, uint64_t items, uint32_t group, 
       hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 4, kD, 1>), grid, dim3(256), 0, stream, args);
     return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
   }
-  // 16-bit caches with groups of 97-128: eight one-tile waves (BF16 128/1,
-  // 8192 tokens: 93.3 -> 88.4 us). Groups of 65-96 stay on three two-tile
+  // 16-bit caches with groups of 97-128: seven or eight one-tile waves (BF16
+  // 128/1, 8192 tokens: 93.3 -> 88.4 us). Groups of 65-96 stay on three two-tile
   // waves: six one-tile waves took 102 us against 70.
   if (!kFp8 && group > 96) {
-    hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 8, kD, 1>), grid, dim3(512), 0, stream, args);
+    // ceil(group / 16) waves, so that every wave holds a live head
+    if (group <= 112)
+      hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 7, kD, 1>), grid, dim3(448), 0, stream, args);
+    else
+      hipLaunchKernelGGL((decode_stream_heads_kernel<QE, kFp8, 8, kD, 1>), grid, dim3(512), 0, stream, args);
     return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
   }
   if (group <= 64) {

@@ -326,7 +326,8 @@ def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
     ((3, 71, 1, 64, 64, 16, [513, 17, 1600]), 512),        # group of 71 at head size 64: three waves, the last 7 heads live
     ((2, 80, 2, 64, 64, 16, [640, 90]), 64),               # group of 40, 64-token partitions: the third wave 8 heads live
     ((2, 33, 1, 128, 128, 16, [300, 1500]), 256),          # group of 33: the third wave one head live
-    ((2, 100, 1, 64, 64, 16, [1000, 70]), 128),            # group of 100: the eighth 16-head wave 4 heads live
+    ((2, 100, 1, 64, 64, 16, [1000, 70]), 128),            # group of 100: seven 16-head waves, the seventh 4 heads live
+    ((2, 113, 1, 128, 128, 16, [700, 1500]), 256),         # group of 113: eight 16-head waves, the eighth 1 head live
 ])
 def test_stream_kernel_wide_groups(dtype, encoding, layout, shape, partition_tokens):
     """Groups of 33-128 query heads per KV head: one workgroup per item, each
