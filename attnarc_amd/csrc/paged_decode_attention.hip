@@ -2479,18 +2479,31 @@ constexpr int kStreamGroupFp8 = 8;
 // are loaded together: the wave starts after two memory round trips, not
 // three. (Compiler-visible scalar loads: the compiler waits for them before
 // any use or copy.)
-// Wave priority rising with the workgroup's place in the grid, in four steps
-// (s_setprio 0-3): of the waves on one CU, those dispatched later, which run
-// the schedule's last and shortest items, get the issue slots first, so the
-// launch's tail is shorter. C3 call 205.3 -> 204.2 us (three pairs, one box);
-// wide groups (B=64, 16384 tokens) BF16 48/1 126.5 -> 124.1, FP8 64/1
-// 127.0 -> 125.1. The FP8 two-partition workgroups measured 0.9 us slower
-// with it (C4) and keep the default priority.
+// Wave priority rising with the workgroup's place in the grid (s_setprio
+// 0-3): of the waves on one CU, those dispatched later, which run the
+// schedule's last and shortest items, get the issue slots first, so the
+// launch's tail is shorter. kSteep: 1 from half the grid, 2 from three
+// quarters, 3 from seven eighths; else one step per quarter. Measured (call
+// us, A/B pairs on one box): C3 205.3 -> 204.2 with quarter steps, 205.0 ->
+// 204.5 steep against quarter steps; wide groups (B=64, 16384 tokens, quarter
+// steps) BF16 48/1 126.5 -> 124.1, FP8 64/1 127.0 -> 125.1, where steep steps
+// measured C5 +2.5 and BF16 48/1 +1.5, but FP8 two-tile waves gain from them
+// (64/1 124.7 -> 118.7, 128/1 at 8192 tokens 110.2 -> 108.7; FP8 48/1 on
+// one-tile waves +1.3). The FP8 two-partition workgroups
+// measured 0.9 us slower with it (C4) and keep the default priority.
+template <bool kSteep>
 __device__ __forceinline__ void rise_priority_with_dispatch() {
-  const uint32_t q = blockIdx.x * 4U / gridDim.x;
-  if (q == 1) __builtin_amdgcn_s_setprio(1);
-  else if (q == 2) __builtin_amdgcn_s_setprio(2);
-  else if (q == 3) __builtin_amdgcn_s_setprio(3);
+  if constexpr (kSteep) {
+    const uint32_t e = blockIdx.x * 8U / gridDim.x;
+    if (e >= 7) __builtin_amdgcn_s_setprio(3);
+    else if (e >= 6) __builtin_amdgcn_s_setprio(2);
+    else if (e >= 4) __builtin_amdgcn_s_setprio(1);
+  } else {
+    const uint32_t q = blockIdx.x * 4U / gridDim.x;
+    if (q == 1) __builtin_amdgcn_s_setprio(1);
+    else if (q == 2) __builtin_amdgcn_s_setprio(2);
+    else if (q == 3) __builtin_amdgcn_s_setprio(3);
+  }
 }
 
 template <typename QE, bool kFp8, int kGroup, uint32_t kD = kDim, int kNt = -1, bool kDirect = false,
@@ -2531,7 +2544,7 @@ void decode_stream_group_kernel(DecodeArgs a) {
     LOOM_WAVE_ITEM(a, item);
     stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item, preloaded, first);
   } else {
-    rise_priority_with_dispatch();
+    rise_priority_with_dispatch<true>();
     const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
     LOOM_WAVE_ITEM(a, item);
     if (!item.valid) return;  // per wave: nothing below waits on the other waves
@@ -2549,7 +2562,7 @@ void decode_stream_heads_kernel(DecodeArgs a) {
   using Dec = StreamDecoder<QE, kFp8, kHTW, kD>;
   __shared__ __attribute__((aligned(16)))
   uint8_t tiles[kSharedStages * Dec::kStageBytes + (kFp8 ? kWaves * kStep * Dec::kPitch : 0)];
-  rise_priority_with_dispatch();
+  rise_priority_with_dispatch<kFp8 && kHTW == 2>();
   LOOM_WAVE_STAMP(blockIdx.x * kWaves + (threadIdx.x >> 6));
   const WorkItem item = schedule_item(a, blockIdx.x);
   if (threadIdx.x < 64) LOOM_WAVE_ITEM(a, item);  // one record per item: the waves share its K/V reads
