@@ -297,13 +297,14 @@ def test_unaligned_output_or_workspace_takes_the_vector_kernel(partition_tokens,
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("encoding", ["native", "fp8"])
 @pytest.mark.parametrize("shape", [
-    (3, 32, 1, 128, 128, 16, [1100, 1, 530]),   # MQA group of 32: two full 16-head tiles
-    (3, 48, 2, 128, 128, 16, [17, 700, 1030]),  # group of 24: the second tile has 8 live heads
+    (3, 32, 1, 128, 128, 16, [1100, 1, 530]),   # MQA group of 32: two full 16-head waves
+    (3, 48, 2, 128, 128, 16, [17, 700, 1030]),  # group of 24: the second wave has 8 live heads
 ])
 @pytest.mark.parametrize("partition_tokens", [512, 0])
 def test_stream_kernel_two_head_tiles(dtype, encoding, shape, partition_tokens):
-    """Groups of 17-32 query heads per KV head on the streaming kernel: both
-    16-head tiles in one wave, sharing the K and V reads."""
+    """Groups of 17-32 query heads per KV head on the streaming kernel: two
+    waves of one 16-head tile each on one shared ring of K/V stages, so the
+    K and V rows are read once for both tiles."""
     B, Hq, Hkv, D, Dv, bs, lengths = shape
     case = case_from(shape, dtype, seed=61, cache_encoding=encoding, partition_tokens=partition_tokens)
     _, _, fam = ops.supports(2, 0, B, Hq, Hkv, D, Dv, case.num_blocks, bs, case.max_blocks_per_sequence,
