@@ -3100,30 +3100,34 @@ int launch_mfma_waves(const DecodeArgs& args, uint64_t grid, uint32_t chunks, hi
                       : launch_mfma<QE, kFp8, kHT, 4>(args, grid, stream);
 }
 
-// The grouped launch pre-merges pairs of partitions in the workgroup when
-// the call is split (more than two partitions, so the states halve), the
-// workgroup holds eight items (FP8 caches: four adjacent KV heads x two
-// partitions) and the KV heads divide into groups of four. One state per
-// pair of partitions halves the split-K state bytes written, which cost far
+// FP8 caches at head size 128 pre-merge pairs of partitions in the
+// workgroup when the call is split (more than two partitions, so the states
+// halve): four-item workgroups of two adjacent KV heads x two partitions
+// (the KV heads divide into twos) leave one state per pair of partitions.
+// One state per pair halves the split-K state bytes written, which cost far
 // more than their share of the traffic: on C3 the F32 state stores (10.5 MB,
 // 0.9% of the bytes) cost the decode kernel 17 us of 205 (188 us with the
-// stores sent to 32 KiB of L2-resident lines). Measured: C4 call 201.8 ->
-// 198.4 us; with four-item 16-bit workgroups (two heads x two partitions)
-// C3 went 205.5 -> 206.9 us, the loss of adjacent heads outweighing the
-// halved writes (189 -> 200 us with the stores sent to L2-resident lines).
-// Head size 128 only. Call us, pairs against one state per partition
-// (B=64, Hq 32 / Hkv 8, 512-token partitions, NHD): FP8 head size 64 117.1
+// stores sent to 32 KiB of L2-resident lines). Measured (C4 call us):
+// eight-item workgroups of four heads x two partitions 201.8 -> 198.4
+// against one state per partition; four-item workgroups of two heads x two
+// partitions then 199.6 -> 194.7 (three pairs; kernel trace 199.1 -> 190.0:
+// three 48 KiB workgroups per CU, where one 96 KiB workgroup per CU ran the
+// launch as four synchronous rounds that dipped at every turnover). 16-bit
+// caches keep one state per partition: two heads x two partitions measured
+// C3 205.5 -> 206.9 us, the loss of four adjacent heads outweighing the
+// halved writes. FP8 at other head sizes neither (call us, pairs against
+// none, B=64, Hq 32 / Hkv 8, 512-token partitions, NHD): head size 64 117.1
 // against 115.3, 80 134.2 against 132.7, 96 131.2 against 129.3, 112 105.5
-// against 104.4, 128 102.9 against 102.9; C4 (HND, 128) 3.4 faster.
-bool pair_eligible(const DecodeArgs& a, int group) {
-  return a.head_size == kDim && a.parts > 2 && group >= 8 && a.kv_heads % static_cast<uint32_t>(group / 2) == 0;
+// against 104.4.
+bool pair_eligible(const DecodeArgs& a, int group, bool fp8) {
+  return fp8 && a.head_size == kDim && a.parts > 2 && group >= 4 && a.kv_heads % static_cast<uint32_t>(group / 2) == 0;
 }
 
 template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup, int kNt = -1, bool kDirect = false>
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   g_launch_kernel = "decode_stream_group_kernel";
-  g_launch_pairs = !kDirect && pair_eligible(args, kGroup);
+  g_launch_pairs = !kDirect && pair_eligible(args, kGroup, kFp8);
   if (g_launch_pairs) {
     // one workgroup per (sequence, pair of partitions, group of kGroup / 2 KV heads)
     const uint64_t units = (args.parts + 1ULL) / 2ULL * args.sequences * (args.kv_heads / (kGroup / 2));
@@ -3495,7 +3499,9 @@ int run_typed(const Problem& p, hipStream_t stream) {
         // The library's own split runs its items in index order with each
         // item's first block IDs loaded alongside its length (C2 decode
         // 18.3-18.5 -> 17.5-17.7 us).
-        status = fp8                  ? launch_stream_group<QE, true, kDim, kStreamGroupFp8>(args, grid, stream)
+        status = fp8 && pair_eligible(args, 4, true)
+                                      ? launch_stream_group<QE, true, kDim, 4>(args, grid, stream)
+                 : fp8                ? launch_stream_group<QE, true, kDim, kStreamGroupFp8>(args, grid, stream)
                  : p.direct_schedule ? launch_stream_group<QE, false, kDim, kStreamGroup, -1, true>(args, grid, stream)
                                      : launch_stream_group<QE, false>(args, grid, stream);
       } else if (steps < 8) {

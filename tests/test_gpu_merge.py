@@ -123,17 +123,18 @@ def test_length_past_max_sequence_length_stays_in_its_share(hq, hkv, dtype):
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse, **LSE_TOL)
 
 
-@pytest.mark.parametrize("head,layout", [(128, "HND"), (128, "NHD"), (64, "HND")])
-def test_fp8_two_partition_workgroups(head, layout):
-    """FP8 grids of 1024+ items at head size 128 run eight-item workgroups of
-    four KV heads x two partitions that leave one state per pair (head size
-    64: one state per partition): sequences that end inside the first
-    partition of a pair, exactly on a pair boundary, one token past it, and
-    single-token ones."""
+@pytest.mark.parametrize("head,layout,hkv", [(128, "HND", 8), (128, "NHD", 8), (64, "HND", 8), (128, "HND", 6),
+                                             (128, "NHD", 3)])
+def test_fp8_two_partition_workgroups(head, layout, hkv):
+    """FP8 grids of 1024+ items at head size 128 run four-item workgroups of
+    two KV heads x two partitions that leave one state per pair (head size
+    64: eight-item workgroups, one state per partition): sequences that end
+    inside the first partition of a pair, exactly on a pair boundary, one
+    token past it, and single-token ones."""
     rng = np.random.default_rng(head)
     lengths = [int(x) for x in rng.integers(1, 4097, 40)]
     lengths[:8] = [1, 511, 512, 513, 1024, 1025, 2048, 4096]
-    case = _case(60 + head, lengths, hq=32, hkv=8, head=head, encoding="fp8", layout=layout, part=256)
+    case = _case(60 + head + hkv, lengths, hq=4 * hkv, hkv=hkv, head=head, encoding="fp8", layout=layout, part=256)
     _check(case, f"fp8 pairs d{head} {layout}")
     from attnarc_amd import ops
 
