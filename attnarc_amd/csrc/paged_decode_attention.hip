@@ -3127,13 +3127,20 @@ template <typename QE, bool kFp8, uint32_t kD = kDim, int kGroup = kStreamGroup,
 int launch_stream_group(const DecodeArgs& args, uint64_t items, hipStream_t stream) {
   TimedLaunch timed(LOOM_HIP_KERNEL_DECODE, stream);
   g_launch_kernel = "decode_stream_group_kernel";
-  g_launch_pairs = !kDirect && pair_eligible(args, kGroup, kFp8);
-  if (g_launch_pairs) {
-    // one workgroup per (sequence, pair of partitions, group of kGroup / 2 KV heads)
-    const uint64_t units = (args.parts + 1ULL) / 2ULL * args.sequences * (args.kv_heads / (kGroup / 2));
-    hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, false, true>),
-                       dim3(static_cast<uint32_t>(units)), dim3(kGroup * 64), 0, stream, args);
-  } else {
+  // Pair workgroups exist only as FP8 four-item workgroups at head size 128
+  // (pair_eligible); other instantiations do not compile the pair path.
+  constexpr bool kMayPair = kFp8 && kGroup == 4 && kD == kDim && !kDirect;
+  g_launch_pairs = kMayPair && pair_eligible(args, kGroup, kFp8);
+  if constexpr (kMayPair) {
+    if (g_launch_pairs) {
+      // one workgroup per (sequence, pair of partitions, group of kGroup / 2 KV heads)
+      const uint64_t units = (args.parts + 1ULL) / 2ULL * args.sequences * (args.kv_heads / (kGroup / 2));
+      hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, false, true>),
+                         dim3(static_cast<uint32_t>(units)), dim3(kGroup * 64), 0, stream, args);
+      return hipGetLastError() == hipSuccess ? LOOM_HIP_SUCCESS : LOOM_HIP_LAUNCH_ERROR;
+    }
+  }
+  {
     const uint64_t groups = (items + kGroup - 1) / kGroup;
     hipLaunchKernelGGL((decode_stream_group_kernel<QE, kFp8, kGroup, kD, kNt, kDirect>),
                        dim3(static_cast<uint32_t>(groups)), dim3(kGroup * 64), 0, stream, args);
