@@ -139,3 +139,20 @@ def test_fp8_two_partition_workgroups(head, layout, hkv):
     from attnarc_amd import ops
 
     assert ops.last_kernel_name() == "decode_stream_group_kernel"
+
+
+@pytest.mark.parametrize("max_len", [2500, 1537])
+def test_fp8_pairs_with_an_odd_partition_count(max_len):
+    """ceil(max_len / 512) = 5 or 4 partitions (3 or 2 pair states): with 5 the
+    last pair has no second partition, and sequences of every length class
+    around the pair boundaries run in the same launch."""
+    rng = np.random.default_rng(max_len)
+    lengths = [int(x) for x in rng.integers(1, max_len + 1, 300)]
+    lengths[:6] = [max_len, 2048, 2049, 1024, 1025, 1]
+    lengths = [min(x, max_len) for x in lengths]
+    case = _case(70 + max_len % 97, lengths, hq=16, hkv=4, encoding="fp8", layout="HND", part=512)
+    assert case.max_sequence_length == max_len
+    _check(case, f"fp8 pairs, max length {max_len}")
+    from attnarc_amd import ops
+
+    assert ops.last_kernel_name() == "decode_stream_group_kernel"
