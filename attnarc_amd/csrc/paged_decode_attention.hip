@@ -1719,6 +1719,9 @@ __device__ unsigned long long g_wave_stall[kWaveRecords][4];
 struct WorkItem {
   uint32_t seq, part, kvh, len;
   bool valid;
+  // schedule_item: the first 64 sequences do not all hold the same number
+  // of full partitions (a ragged batch)
+  bool uneven = false;
 };
 
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x, uint32_t lane) {
@@ -1791,6 +1794,8 @@ __device__ __forceinline__ WorkItem schedule_item(const DecodeArgs& a, uint32_t 
       const uint32_t len = static_cast<uint32_t>(min(static_cast<uint64_t>(lengths_chunk(a, c0, lane)),
                                                      static_cast<uint64_t>(a.parts) * pt));
       const uint32_t full = len / pt;
+      if (cls == 0 && c0 == 0)
+        it.uneven = __builtin_amdgcn_ballot_w64(lane < a.sequences && full != __builtin_amdgcn_readfirstlane(full)) != 0;
       const uint32_t n = cls == 0 ? full : (len % pt != 0 ? 1U : 0U);
       const uint32_t incl = wave_inclusive_sum(n, lane);
       const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
@@ -2483,9 +2488,14 @@ constexpr int kStreamGroupFp8 = 8;
 // 0-3): of the waves on one CU, those dispatched later, which run the
 // schedule's last and shortest items, get the issue slots first, so the
 // launch's tail is shorter. kSteep: 1 from half the grid, 2 from three
-// quarters, 3 from seven eighths; else one step per quarter. Measured (call
+// quarters, 3 from seven eighths; else one step per quarter. The grouped
+// kernel applies it only to ragged batches (WorkItem::uneven): where every
+// item is the same length the later workgroups starve the earlier ones on
+// their CUs (B=64 x 4096 tokens, Hq 32 / Hkv 8: head size 128 175.5 ->
+// 186.7 us per call, 96 187.1 -> 200.5, 112 171.8 -> 185.3). Measured (call
 // us, A/B pairs on one box): C3 205.3 -> 204.2 with quarter steps, 205.0 ->
-// 204.5 steep against quarter steps; wide groups (B=64, 16384 tokens, quarter
+// 204.5 steep against quarter steps, 205.5 -> 204.5 steep on ragged batches
+// only; wide groups (B=64, 16384 tokens, quarter
 // steps) BF16 48/1 126.5 -> 124.1, FP8 64/1 127.0 -> 125.1, where steep steps
 // measured C5 +2.5 and BF16 48/1 +1.5, but FP8 two-tile waves gain from them
 // (64/1 124.7 -> 118.7, 128/1 at 8192 tokens 110.2 -> 108.7; FP8 48/1 on
@@ -2544,8 +2554,8 @@ void decode_stream_group_kernel(DecodeArgs a) {
     LOOM_WAVE_ITEM(a, item);
     stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item, preloaded, first);
   } else {
-    rise_priority_with_dispatch<true>();
     const WorkItem item = schedule_item(a, blockIdx.x * kGroup + wave);
+    if (item.uneven) rise_priority_with_dispatch<true>();
     LOOM_WAVE_ITEM(a, item);
     if (!item.valid) return;  // per wave: nothing below waits on the other waves
     stream_item<QE, kFp8, 1, 1, kD, kGroupStages, kNt>(a, tiles + wave * Dec::kWaveBytes, item);
