@@ -2474,7 +2474,8 @@ constexpr int kStreamGroupStages = 2;
 // 128 KiB per CU). With non-temporal K/V loads and partial stores, four
 // against eight: C4 decode 189.4-189.9 against 189.6-190.1 us (the same);
 // head size 96 82.9-84.2 against 79.9-80.3, 112 89.7-90.2 against 84.9-85.3
-// (eight faster).
+// (eight faster). Head size 128 with more than two partitions takes four-item
+// workgroups that fold pairs of partitions instead (pair_eligible).
 constexpr int kStreamGroupFp8 = 8;
 
 // kDirect: items in index order (KV head fastest, then partition, then
